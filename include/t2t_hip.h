@@ -1,0 +1,218 @@
+/*
+ * Token2Tile sparse attention on MI355X (gfx950): the C ABI.
+ *
+ * Every entry point is destination passing: the caller allocates inputs,
+ * outputs and workspaces in device memory and passes plain pointers, sizes
+ * and a HIP stream (hipStream_t, passed as void*; NULL = the null stream).
+ * Work is enqueued on that stream; nothing synchronises the host.  Each
+ * function returns T2T_OK or an error code; t2t_last_error() gives a message
+ * for the calling thread's last failure.  Inputs are never modified.
+ *
+ * Layouts (H heads, N tokens, D = 128 head dim, r = 32 rank, CK = 2048 key
+ * clusters, CQ query clusters), all row-major and contiguous:
+ *   q, k, v, kp, V_sorted, attn_out, out   [H, N, D]   fp16 or bf16 (dtype)
+ *   QU, KU                                 [H, N, r]   fp16
+ *   U (Uq / Uk)                            [H, D, r]   fp16
+ *   cq                                     [H, CQ, r]  fp16
+ *   ck0, ck16, cks                         [H, CK, r]  fp16;  ck2 fp32
+ *   gl                                     [H, N, CK]  fp16
+ *   labels / perms / rowcnt                [H, N]      int32
+ *   counts                                 [H, CQ] or [H, CK] int32
+ *   unip (packed union)                    [H, CQ, CK/32] int32, bit c&31
+ *                                          of word c>>5 = cluster c
+ *   sumv                                   [H, CK, D]  fp16;  lam [H] fp32
+ *   lse                                    [H, N] fp32 (log2 units)
+ *
+ * Reference citations are relative to the Token2Tile source tree
+ * (token2tile/operator/...).
+ */
+#ifndef T2T_HIP_H
+#define T2T_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes and data types ------------------------------------- */
+#define T2T_OK            0
+#define T2T_ERR_ARG       1   /* bad size, pointer or dtype            */
+#define T2T_ERR_WORKSPACE 2   /* workspace missing or too small        */
+#define T2T_ERR_LAUNCH    3   /* the HIP runtime rejected a launch     */
+#define T2T_ERR_UNSUPPORTED 4 /* shape outside the kernels' limits     */
+
+#define T2T_F16  0
+#define T2T_BF16 1
+
+/* Message for the calling thread's last non-zero return. */
+const char* t2t_last_error(void);
+/* ABI version (major * 100 + minor). */
+int t2t_abi_version(void);
+
+/* ---- S1 projection --------------------------------------------------- */
+/* out[h, n, :] = fp16(x[h, n, :] @ U[h]) with fp32 accumulation; bf16 x is
+ * rounded to fp16 first, as the reference backend casts bf16 to fp16.
+ * Replaces torch.bmm(q, Uq, out=QU) / torch.bmm(k, Uk, out=KU),
+ * operator/deploy_step.py:321-324.  D % 16 == 0, D <= 256, r == 32. */
+int t2t_project(const void* x, int x_dtype, const void* U, void* out,
+                int H, int N, int D, int r, void* stream);
+
+/* ---- S2 k-means maintenance ------------------------------------------ */
+/* Workspace bytes for t2t_kmm_run. */
+size_t t2t_kmm_ws_bytes(int H, int N, int CQ, int CK);
+/* One warm-started k-means update: query labels over two assignment passes
+ * (qlab, cq2, qcounts, qperm), key labels in one pass (klab, kcounts,
+ * kperm, ck2 fp32), cluster-ordered V (V_sorted, dtype v_dtype), value sums
+ * sumv = fp16(vsum / lam) with lam = max(1, max|vsum| / 32768).  Rows
+ * >= N - pin_tail get key label CK - 1.  Deterministic.
+ * Replaces kmm_ext.run, kernels/kmeans_maintain/src/main.cpp:20-46
+ * (kernels.cu:787-876).  r == 32, 1 <= CQ <= 4096, 1 <= CK <= 4096. */
+int t2t_kmm_run(const void* QU, const void* KU, const void* V, int v_dtype,
+                const void* cq0, const void* ck0,
+                int32_t* qlab, void* cq2, int32_t* klab, float* ck2,
+                int32_t* qcounts, int32_t* qperm,
+                int32_t* kcounts, int32_t* kperm,
+                void* V_sorted, void* sumv, float* lam,
+                int H, int N, int CQ, int CK, int pin_tail,
+                void* ws, size_t ws_bytes, void* stream);
+/* Workspace bytes for the two value-statistics calls. */
+size_t t2t_vstats_ws_bytes(int H, int N, int CK);
+/* Reuse call: V_sorted = V[kperm], sumv, lam from this call's V.
+ * Replaces kmm_ext.run_vstats_gather, kmeans_maintain/src/main.cpp:63-78
+ * (kernels.cu:900-923). */
+int t2t_kmm_run_vstats_gather(const void* V, int v_dtype,
+                              const int32_t* kperm, const int32_t* kcounts,
+                              void* V_sorted, void* sumv, float* lam,
+                              int H, int N, int CK,
+                              void* ws, size_t ws_bytes, void* stream);
+/* sumv, lam from an already cluster-ordered V_sorted.
+ * Replaces kmm_ext.run_vstats, kmeans_maintain/src/main.cpp:48-61. */
+int t2t_kmm_run_vstats(const void* V_sorted, int v_dtype,
+                       const int32_t* kcounts, void* sumv, float* lam,
+                       int H, int N, int CK,
+                       void* ws, size_t ws_bytes, void* stream);
+
+/* ---- S3 centroids and scores ----------------------------------------- */
+/* ck16 = fp16(ck2); cks = fp16(fp32(ck2 * scale)).
+ * Replaces state["ck"] = ck2.half() and cks = (ck2 * scale).half(),
+ * operator/deploy_step.py:389,393. Either output may be NULL. */
+int t2t_centroid_finalize(const float* ck2, void* ck16, void* cks, float scale,
+                          int H, int CK, int r, void* stream);
+/* gl[h, n, c] = fp16(QU[h, n] . cks[h, c]) with fp32 accumulation.
+ * Replaces torch.bmm(QU, cks^T, out=gl), operator/deploy_step.py:394.
+ * r == 32, CK % 256 == 0. */
+int t2t_score(const void* QU, const void* cks, void* gl,
+              int H, int N, int CK, int r, void* stream);
+
+/* ---- S4 selection and union ------------------------------------------ */
+/* Workspace bytes for the selection calls. */
+size_t t2t_select_ws_bytes(int H, int N, int CQ);
+/* Per query row: the shortest prefix of key clusters, ordered by score
+ * descending (fp16 bit order, -0 < +0) then cluster index ascending, whose
+ * sizes reach ns (read from device memory, *ns_dev).  unip ORs the
+ * selections of the rows qperm[off[t] : off[t] + qcounts[t]] of every query
+ * cluster t (off = exclusive scan of qcounts); rowcnt[h, row] = selected
+ * keys of that row.  Requires 1 <= ns <= N, N < 524288, CK == 2048.
+ * Replaces ext.run_packed, kernels/select_union/src/main.cpp:40-53
+ * (kernel.cu:76-97,190-412,447-488,523-537). */
+int t2t_select_run_packed(const void* gl, const int32_t* kcounts,
+                          const int32_t* qperm, const int32_t* qcounts,
+                          const int32_t* ns_dev, int32_t* unip, int32_t* rowcnt,
+                          int H, int N, int CQ,
+                          void* ws, size_t ws_bytes, void* stream);
+/* The split variant: same bitmap (rows are processed in balanced chunks
+ * whatever the query cluster sizes); cap >= 1 is validated and recorded.
+ * Replaces ext.run_split_packed, select_union/src/main.cpp:55-72. */
+int t2t_select_run_split_packed(const void* gl, const int32_t* kcounts,
+                                const int32_t* qperm, const int32_t* qcounts,
+                                int cap, const int32_t* ns_dev,
+                                int32_t* unip, int32_t* rowcnt,
+                                int H, int N, int CQ,
+                                void* ws, size_t ws_bytes, void* stream);
+/* Byte-per-cluster union uni[h, t, c] in {0, 1}, [H, CQ, CK] uint8.
+ * Replaces ext.run, select_union/src/main.cpp:5-19 (kernel.cu:414-440). */
+int t2t_select_run(const void* gl, const int32_t* kcounts,
+                   const int32_t* qperm, const int32_t* qcounts,
+                   const int32_t* ns_dev, uint8_t* uni, int32_t* rowcnt,
+                   int H, int N, int CQ,
+                   void* ws, size_t ws_bytes, void* stream);
+/* Sets bit CK-1 of every union word row (pinned context cluster).
+ * Replaces operator/deploy_step.py:444-448. */
+int t2t_union_or_last(int32_t* unip, int H, int CQ, int CK, void* stream);
+
+/* ---- gather ----------------------------------------------------------- */
+/* out[h, i, :] = x[h, perm[h, i], :].  Replaces fast_gather,
+ * operator/fast_permute.py:54-56.  D * elem_size % 16 == 0. */
+int t2t_fast_gather(const void* x, int dtype, const int32_t* perm, void* out,
+                    int H, int N, int D, void* stream);
+
+/* ---- S5/S6 tile attention, residual and merge ------------------------- */
+/* int32 elements of a task plan (workspace owned by a structure snapshot).
+ * Mirrors plan_workspace_ints, kernels/tile_attn/src/main.cpp:16-22. */
+size_t t2t_tile_plan_ints(int H, int N, int CQ);
+/* Task plan: key-cluster offsets, union lengths, per-head task list ordered
+ * by descending rows x kv_len (ties: lower index first).
+ * Replaces the plan kernels, tile_attn/src/kernel.cu:259-378,1123-1130. */
+int t2t_tile_plan(const int32_t* qcounts, const int32_t* kcounts,
+                  const int32_t* unip, int32_t* plan,
+                  int H, int N, int CQ, void* stream);
+/* Exact attention of each query cluster over its union (S5).  q in the
+ * original order, kp/vp cluster ordered; attn_out [H, N, D] (dtype) and
+ * lse [H, N] fp32 in the SORTED query order (position j = qperm order).
+ * Empty union: zeros and lse = -inf.  Needs a plan from t2t_tile_plan.
+ * Replaces launch_cluster_attn, tile_attn/src/kernel.cu:1101-1138. */
+int t2t_tile_attn_exact(const void* q, const void* kp, const void* vp, int dtype,
+                        const int32_t* kcounts, const int32_t* unip, const int32_t* qperm,
+                        const int32_t* plan, void* attn_out, float* lse,
+                        int H, int N, int CQ, void* stream);
+/* Centroid residual over the clusters outside each query's union and the
+ * merge with the exact part under one softmax (S6); out in the ORIGINAL
+ * order.  tailw_dev: 0-dim fp32 on device.
+ * Replaces launch_tail_merge, tile_attn/src/kernel.cu:1478-1495. */
+int t2t_tail_merge(const void* attn_out, const float* lse, const void* QU,
+                   const void* cks, const void* sumv, const int32_t* kcounts,
+                   const int32_t* unip, const int32_t* qlab,
+                   const int32_t* qperm, const float* lam, const float* tailw_dev,
+                   void* out, int dtype, int H, int N, int CQ, void* stream);
+/* attn_out/lse workspace bytes for t2t_tile_attn_run(_planned). */
+size_t t2t_tile_attn_ws_bytes(int H, int N, int dtype);
+/* Plan (when rebuild_plan != 0), exact attention, residual and merge in
+ * one call.  Replaces tile_attn_ext.run_planned,
+ * kernels/tile_attn/src/main.cpp:67-79; ws holds attn_out and lse (the
+ * reference allocates them per call). */
+int t2t_tile_attn_run_planned(const void* q, const void* kp, const void* vp, int dtype,
+                              const int32_t* qcounts, const int32_t* kcounts,
+                              const int32_t* unip, const void* QU, const void* cks,
+                              const void* sumv, const float* lam,
+                              const int32_t* qlab, const int32_t* qperm,
+                              const float* tailw_dev, void* out,
+                              int32_t* plan, int rebuild_plan,
+                              int H, int N, int CQ,
+                              void* ws, size_t ws_bytes, void* stream);
+
+/* ---- init_state helpers ----------------------------------------------- */
+/* labels[h, n] = nearest centroid of x[h, n] (||x||^2 - 2 x.c + ||c||^2,
+ * fp32, lowest index on ties).  Replaces fast_assign,
+ * operator/fast_assign.py:79-106.  D % 16 == 0, D <= 128, C <= 4096. */
+int t2t_fast_assign(const void* x, const void* c, int32_t* labels,
+                    int H, int N, int C, int D, void* stream);
+/* Workspace bytes for t2t_det_centroid_update. */
+size_t t2t_det_update_ws_bytes(int H, int N, int C);
+/* Deterministic centroid update: int64 fixed-point (2^-20) sums per
+ * cluster, mean in fp64, cast to fp16 through fp32; empty clusters keep old.
+ * Replaces _det_centroid_update, integrations/sglang/backend/t2t_attn.py:242-257. */
+int t2t_det_centroid_update(const void* x, const int32_t* labels, const void* old,
+                            void* out, int32_t* counts,
+                            int H, int N, int C, int D,
+                            void* ws, size_t ws_bytes, void* stream);
+/* G[h] = x[h]^T x[h] / N in fp64 ([H, D, D]); bf16 x is rounded to fp16
+ * first.  Replaces the Gram products of online_u,
+ * operator/deploy_step.py:135-137. D <= 128. */
+int t2t_gram(const void* x, int x_dtype, double* G, int H, int N, int D, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* T2T_HIP_H */

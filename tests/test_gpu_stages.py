@@ -1,0 +1,339 @@
+"""Stage-by-stage parity of the HIP kernels with the CPU oracle.
+
+Integer / index work is compared bit-exactly given identical inputs; MMA
+products (projection, scores) within 1 fp16 ulp; attention outputs within
+the stated tolerances.  Each stage is fed the same inputs on both sides
+(the GPU's previous-stage outputs where a stage has an MMA-rounded input).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import t2t_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def g(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def c(t):
+    return t.detach().cpu().numpy()
+
+
+def within_ulp(a16, b16, ulps=1):
+    a = a16.astype(np.float32)
+    b = b16.astype(np.float32)
+    sp = np.spacing(np.abs(b16.astype(np.float16))).astype(np.float32)
+    return np.all(np.abs(a - b) <= ulps * sp + 1e-7)
+
+
+def clustered(rng, H, N, r, C, spread=0.05):
+    """Points near centroids: labels are unambiguous (no near ties)."""
+    cent = rng.normal(0, 1, (H, C, r)).astype(np.float16)
+    lab = rng.integers(0, C, (H, N))
+    x = np.take_along_axis(cent.astype(np.float64), lab[..., None], 1)
+    x = (x + spread * rng.normal(0, 1, (H, N, r))).astype(np.float16)
+    return x, cent, lab
+
+
+# ---------------------------------------------------------------------------
+def test_project_f16_bf16(dev):
+    from token2tile_amd import ops
+    rng = np.random.default_rng(0)
+    H, N = 2, 1000
+    x = rng.normal(0, 1, (H, N, 128)).astype(np.float16)
+    U = (rng.normal(0, 1, (H, 128, 32)) / 8).astype(np.float16)
+    out = c(ops.project(g(x, dev), g(U, dev)))
+    assert within_ulp(out, O.project(x, U))
+    xb = g(x, dev).to(torch.bfloat16)
+    outb = c(ops.project(xb, g(U, dev)))
+    xr = c(xb.float()).astype(np.float16)          # bf16 -> fp16 as the backend cast
+    assert within_ulp(outb, O.project(xr, U))
+
+
+def test_score_and_finalize(dev):
+    from token2tile_amd import ops
+    rng = np.random.default_rng(1)
+    H, N = 2, 777
+    QU = rng.normal(0, 1, (H, N, 32)).astype(np.float16)
+    ck2 = rng.normal(0, 1, (H, 2048, 32)).astype(np.float32)
+    ck16, cks = ops.centroid_finalize(g(ck2, dev))
+    e16, ecks = O.scale_centroids(ck2)
+    assert np.array_equal(c(ck16), e16) and np.array_equal(c(cks), ecks)
+    gl = c(ops.score(g(QU, dev), cks))
+    assert within_ulp(gl, O.scores(QU, ecks))
+
+
+def test_gather_and_union_bit(dev):
+    from token2tile_amd import ops
+    rng = np.random.default_rng(2)
+    x = rng.normal(0, 1, (3, 500, 128)).astype(np.float16)
+    perm = np.stack([rng.permutation(500) for _ in range(3)]).astype(np.int32)
+    out = c(ops.fast_gather(g(x, dev), g(perm, dev)))
+    assert np.array_equal(out, np.stack([x[h][perm[h]] for h in range(3)]))
+    xb = g(x, dev).to(torch.bfloat16)
+    assert torch.equal(ops.fast_gather(xb, g(perm, dev)).cpu(),
+                       torch.stack([xb[h][g(perm, dev)[h].long()] for h in range(3)]).cpu())
+    u = torch.zeros(2, 5, 64, dtype=torch.int32, device=dev)
+    ops.union_or_last(u)
+    assert np.array_equal(c(u), O.or_pin_tail(np.zeros((2, 5, 64), dtype=np.int32)))
+
+
+# ---------------------------------------------------------------------------
+SEL_CASES = ["normal", "coarse", "tied", "signedzero", "zeros", "nan"]
+
+
+def sel_inputs(rng, kind, H, N, CQ):
+    sizes = np.stack([rng.multinomial(N, np.ones(2048) / 2048) for _ in range(H)]).astype(np.int32)
+    if kind == "zeros":
+        for h in range(H):
+            z = rng.choice(2048, 1500, replace=False)
+            moved = sizes[h, z].sum()
+            sizes[h, z] = 0
+            sizes[h, rng.choice(np.setdiff1d(np.arange(2048), z))] += moved
+    if kind in ("normal", "zeros", "nan"):
+        gl = rng.normal(0, 1, (H, N, 2048)).astype(np.float16)
+        if kind == "nan":
+            gl[0, :5, 100] = np.nan
+    elif kind == "coarse":
+        gl = (np.round(rng.normal(0, 1, (H, N, 2048)) * 4) / 4).astype(np.float16)
+    elif kind == "tied":
+        gl = np.full((H, N, 2048), 0.25, dtype=np.float16)
+    else:
+        gl = rng.choice(np.array([0.0, -0.0, 1.0, -1.0], dtype=np.float16), (H, N, 2048))
+    qlab = rng.integers(0, CQ - 1, (H, N)).astype(np.int32)   # cluster CQ-1 stays empty
+    qlab[:, :3] = 0
+    qperm, qcounts = O.stable_perm(qlab, CQ)
+    return gl, sizes, qperm, qcounts
+
+
+@pytest.mark.parametrize("kind", SEL_CASES)
+@pytest.mark.parametrize("ns", [1, 300, 4096])
+def test_select_union_bit_exact(dev, kind, ns):
+    from token2tile_amd import ops
+    rng = np.random.default_rng(hash((kind, ns)) % (2 ** 32))
+    H, N, CQ = 2, 4096, 24
+    gl, sizes, qperm, qcounts = sel_inputs(rng, kind, H, N, CQ)
+    ns_t = torch.tensor(ns, dtype=torch.int32, device=dev)
+    unip, rowcnt = ops.select_union(g(gl, dev), g(sizes, dev), g(qperm, dev), g(qcounts, dev), ns_t)
+    eu, er = O.select_union(gl, sizes, qperm, qcounts, ns)
+    assert np.array_equal(c(rowcnt), er)
+    assert np.array_equal(c(unip), eu)
+    u2, r2 = ops.select_union(g(gl, dev), g(sizes, dev), g(qperm, dev), g(qcounts, dev), ns_t,
+                              split_cap=37)
+    assert torch.equal(u2, unip) and torch.equal(r2, rowcnt)
+    ub, rb = ops.select_union_bytes(g(gl, dev), g(sizes, dev), g(qperm, dev), g(qcounts, dev), ns_t)
+    assert np.array_equal(c(ub).astype(bool), O.unpack_bits(eu))
+
+
+def test_select_one_query_per_cluster_and_full_budget(dev):
+    from token2tile_amd import ops
+    rng = np.random.default_rng(9)
+    H, N, CQ = 1, 512, 512
+    gl = rng.normal(0, 1, (H, N, 2048)).astype(np.float16)
+    sizes = rng.multinomial(N, np.ones(2048) / 2048)[None].astype(np.int32)
+    qlab = rng.permutation(N)[None].astype(np.int32)
+    qperm, qcounts = O.stable_perm(qlab, CQ)
+    for ns in (1, N):
+        ns_t = torch.tensor(ns, dtype=torch.int32, device=dev)
+        unip, rowcnt = ops.select_union(g(gl, dev), g(sizes, dev), g(qperm, dev), g(qcounts, dev),
+                                        ns_t)
+        eu, er = O.select_union(gl, sizes, qperm, qcounts, ns)
+        assert np.array_equal(c(unip), eu) and np.array_equal(c(rowcnt), er)
+
+
+# ---------------------------------------------------------------------------
+def test_kmeans_clear_clusters_exact(dev):
+    """Well-separated data: labels agree exactly, so every output must be
+    bit-identical to the oracle's."""
+    from token2tile_amd import ops
+    rng = np.random.default_rng(3)
+    H, N, CQ, CK = 2, 6000, 64, 2048
+    QU, cq0, _ = clustered(rng, H, N, 32, CQ)
+    KU, ck0, _ = clustered(rng, H, N, 32, CK, spread=0.02)
+    V = rng.normal(0, 1, (H, N, 128)).astype(np.float16)
+    for pin in (0, 100):
+        o = ops.kmm_run(g(QU, dev), g(KU, dev), g(V, dev), g(cq0, dev), g(ck0, dev), pin_tail=pin)
+        e = O.kmeans_maintain(QU, KU, V, cq0, ck0, pin_tail=pin)
+        for k in ("qlab", "qcounts", "qperm", "cq2", "klab", "kcounts", "kperm", "ck2", "V_sorted",
+                  "sumv", "lam"):
+            assert np.array_equal(c(o[k]), e[k]), (pin, k)
+
+
+def test_kmeans_labels_near_ties_only_and_chained_exact(dev):
+    """Random data: label disagreements only at near-ties; everything
+    downstream of the GPU's labels is bit-exact."""
+    from token2tile_amd import ops
+    rng = np.random.default_rng(4)
+    H, N, CQ, CK = 2, 5000, 96, 2048
+    QU = rng.normal(0, 1, (H, N, 32)).astype(np.float16)
+    KU = rng.normal(0, 1, (H, N, 32)).astype(np.float16)
+    cq0 = QU[:, rng.choice(N, CQ, replace=False)]
+    ck0 = KU[:, rng.choice(N, CK, replace=False)]
+    V = rng.normal(0, 1, (H, N, 128)).astype(np.float16)
+    o = ops.kmm_run(g(QU, dev), g(KU, dev), g(V, dev), g(cq0, dev), g(ck0, dev))
+    klab = c(o["klab"])
+    d = O.assign_distances(KU, ck0)
+    dmin = d.min(-1)
+    mine = np.take_along_axis(d, klab[..., None].astype(np.int64), -1)[..., 0]
+    assert np.all(mine - dmin <= 1e-4 * (1 + np.abs(dmin)))
+    assert (klab != O.assign(KU, ck0)).mean() < 1e-3
+    ks = O.key_side(KU, V, ck0, klab)
+    for k in ("kcounts", "kperm", "ck2", "V_sorted", "sumv", "lam"):
+        assert np.array_equal(c(o[k]), ks[k]), k
+    qlab = c(o["qlab"])
+    qperm, qcounts = O.stable_perm(qlab, CQ)
+    assert np.array_equal(c(o["qperm"]), qperm) and np.array_equal(c(o["qcounts"]), qcounts)
+
+
+def test_vstats_reuse_paths(dev):
+    from token2tile_amd import ops
+    rng = np.random.default_rng(5)
+    H, N = 2, 3000
+    V = rng.normal(0, 3, (H, N, 128)).astype(np.float16)
+    klab = rng.integers(0, 2000, (H, N)).astype(np.int32)
+    kperm, kcounts = O.stable_perm(klab, 2048)
+    eVs, esumv, elam, _ = O.v_statistics(V, kperm, kcounts)
+    Vs, sumv, lam = ops.vstats_gather(g(V, dev), g(kperm, dev), g(kcounts, dev))
+    assert np.array_equal(c(Vs), eVs) and np.array_equal(c(sumv), esumv)
+    assert np.array_equal(c(lam), elam)
+    sumv2, lam2 = ops.vstats(Vs, g(kcounts, dev))
+    assert torch.equal(sumv2, sumv) and torch.equal(lam2, lam)
+    Vb = g(V, dev).to(torch.bfloat16)
+    Vsb, sumvb, lamb = ops.vstats_gather(Vb, g(kperm, dev), g(kcounts, dev))
+    eVs2, esumv2, elam2, _ = O.v_statistics(c(Vb.float()), kperm, kcounts)
+    assert np.array_equal(c(Vsb.float()), eVs2) and np.array_equal(c(sumvb), esumv2)
+
+
+def test_init_helpers(dev):
+    from token2tile_amd import ops
+    rng = np.random.default_rng(6)
+    x, cent, lab = clustered(rng, 2, 3000, 32, 100)
+    got = c(ops.fast_assign_labels(g(x, dev), g(cent, dev)))
+    assert np.array_equal(got, O.fast_assign(x, cent))
+    new, counts = ops.det_centroid_update(g(x, dev), g(got, dev), g(cent, dev))
+    en, ec = O.det_centroid_update(x, got, cent)
+    assert np.array_equal(c(new), en) and np.array_equal(c(counts), ec)
+    G = c(ops.gram(g(x, dev)))
+    xd = x.astype(np.float64)
+    assert np.allclose(G, np.einsum("hni,hnj->hij", xd, xd) / x.shape[1], rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+def attn_case(rng, H=2, N=3000, CQ=24, density=0.1, empty_cluster=True):
+    q = rng.normal(0, 1, (H, N, 128)).astype(np.float16)
+    k = rng.normal(0, 1, (H, N, 128)).astype(np.float16)
+    v = rng.normal(0, 1, (H, N, 128)).astype(np.float16)
+    klab = rng.integers(0, 2048, (H, N)).astype(np.int32)
+    kperm, kcounts = O.stable_perm(klab, 2048)
+    qlab = rng.integers(0, CQ, (H, N)).astype(np.int32)
+    if empty_cluster:
+        qlab[qlab == 5] = 6
+    qlab[:, :300] = 7                                        # one large cluster (> 128 rows)
+    qperm, qcounts = O.stable_perm(qlab, CQ)
+    sel = rng.random((H, CQ, 2048)) < density
+    sel[:, 3] = False                                        # an empty union
+    sel[:, 4] = True                                         # a full union
+    unip = O.pack_bits(sel)
+    kp = np.stack([k[h][kperm[h]] for h in range(H)])
+    vp = np.stack([v[h][kperm[h]] for h in range(H)])
+    return q, k, v, kperm, kcounts, qlab, qperm, qcounts, unip, kp, vp
+
+
+def test_plan(dev):
+    from token2tile_amd import ops
+    rng = np.random.default_rng(7)
+    q, k, v, kperm, kcounts, qlab, qperm, qcounts, unip, kp, vp = attn_case(rng)
+    H, N, _ = q.shape
+    CQ = qcounts.shape[1]
+    plan = ops.tile_plan(g(qcounts, dev), g(kcounts, dev), g(unip, dev), N)
+    pv = {k_: c(v_) for k_, v_ in ops.plan_views(plan, H, N, CQ).items()}
+    assert np.array_equal(pv["k_off"][:, :2048], O.exclusive_scan(kcounts))
+    uni = O.unpack_bits(unip)
+    kvlen = np.where(qcounts > 0, (uni * kcounts[:, None, :]).sum(-1), 0)
+    assert np.array_equal(pv["kvlen"], kvlen)
+    qoff = O.exclusive_scan(qcounts)
+    for h in range(H):
+        nt = pv["ntask"][h]
+        tasks = pv["tasks"][h, :nt]
+        covered = np.zeros(N, dtype=int)
+        for t, s, rows, _ in tasks:
+            assert 1 <= rows <= 128 and qoff[h, t] <= s and s + rows <= qoff[h, t] + qcounts[h, t]
+            covered[s:s + rows] += 1
+        assert np.all(covered == 1)
+        work = tasks[:, 2].astype(np.int64) * kvlen[h, tasks[:, 0]]
+        assert np.all(np.diff(work) <= 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_tile_attention_exact(dev, dtype):
+    from token2tile_amd import ops
+    rng = np.random.default_rng(8)
+    q, k, v, kperm, kcounts, qlab, qperm, qcounts, unip, kp, vp = attn_case(rng)
+    H, N, _ = q.shape
+    tq, tkp, tvp = (g(a, dev).to(dtype) for a in (q, kp, vp))
+    plan = ops.tile_plan(g(qcounts, dev), g(kcounts, dev), g(unip, dev), N)
+    ao, lse = ops.tile_attn_exact(tq, tkp, tvp, g(kcounts, dev), g(unip, dev), g(qperm, dev), plan)
+    qf, kpf, vpf = (c(t.float()) for t in (tq, tkp, tvp))
+    eo, el = O.tile_attention(qf, kpf, vpf, qcounts, kcounts, unip, qperm)
+    got = c(ao.float())
+    tol = 4e-3 if dtype == torch.float16 else 2e-2
+    assert np.abs(got - eo).max() < tol
+    fin = np.isfinite(el)
+    assert np.array_equal(fin, np.isfinite(c(lse)))
+    assert np.abs(c(lse)[fin] - el[fin]).max() < 2e-3
+    assert np.all(got[~fin] == 0)
+
+
+def test_full_union_equals_sdpa(dev):
+    from token2tile_amd import ops
+    rng = np.random.default_rng(10)
+    H, N, CQ = 2, 2048, 16
+    q = torch.randn(H, N, 128, device=dev, dtype=torch.bfloat16)
+    k = torch.randn(H, N, 128, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(H, N, 128, device=dev, dtype=torch.bfloat16)
+    klab = rng.integers(0, 2048, (H, N)).astype(np.int32)
+    kperm, kcounts = O.stable_perm(klab, 2048)
+    qlab = rng.integers(0, CQ, (H, N)).astype(np.int32)
+    qperm, qcounts = O.stable_perm(qlab, CQ)
+    unip = O.pack_bits(np.ones((H, CQ, 2048), dtype=bool))
+    kp = ops.fast_gather(k, g(kperm, dev))
+    vp = ops.fast_gather(v, g(kperm, dev))
+    plan = ops.tile_plan(g(qcounts, dev), g(kcounts, dev), g(unip, dev), N)
+    ao, lse = ops.tile_attn_exact(q, kp, vp, g(kcounts, dev), g(unip, dev), g(qperm, dev), plan)
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float())
+    ref_sorted = torch.stack([ref[h][g(qperm, dev)[h].long()] for h in range(H)])
+    assert (ao.float() - ref_sorted).abs().max().item() < 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_tail_merge(dev, dtype):
+    from token2tile_amd import ops
+    rng = np.random.default_rng(11)
+    H, N, CQ = 2, 1500, 12
+    QU = rng.normal(0, 1, (H, N, 32)).astype(np.float16)
+    cks = (rng.normal(0, 1, (H, 2048, 32)) * 0.3).astype(np.float16)
+    sumv = rng.normal(0, 2, (H, 2048, 128)).astype(np.float16)
+    kcounts = rng.integers(0, 5, (H, 2048)).astype(np.int32)
+    qlab = rng.integers(0, CQ, (H, N)).astype(np.int32)
+    qperm, qcounts = O.stable_perm(qlab, CQ)
+    sel = rng.random((H, CQ, 2048)) < 0.2
+    sel[:, 0] = False
+    sel[:, 1] = True
+    unip = O.pack_bits(sel)
+    ao = torch.randn(H, N, 128, device=dev).to(dtype)
+    lse = (torch.randn(H, N, device=dev) + 12.0)
+    lse[:, :40] = -float("inf")
+    lam = np.array([1.0, 2.5], dtype=np.float32)
+    tw = torch.tensor(1.0, device=dev)
+    out = ops.tail_merge(ao, lse, g(QU, dev), g(cks, dev), g(sumv, dev), g(kcounts, dev),
+                         g(unip, dev), g(qlab, dev), g(qperm, dev), g(lam, dev), tw)
+    eo = O.tail_merge(c(ao.float()).astype(np.float64), c(lse).astype(np.float64), QU, cks, sumv,
+                      kcounts, unip, qlab, qperm, lam, 1.0)
+    got = c(out.float())
+    tol = 5e-3 if dtype == torch.float16 else 3e-2
+    assert np.abs(got - eo).max() < tol * max(1.0, np.abs(eo).max())

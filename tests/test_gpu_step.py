@@ -1,0 +1,120 @@
+"""Whole-call parity: MaskedStepDeploy.step on the GPU against the CPU oracle
+on identical seeded inputs and identical state (full call, reuse call,
+fp16 and bf16 inputs, pinned tail), plus determinism."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import t2t_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def cos(a, b):
+    a = a.ravel().astype(np.float64)
+    b = b.ravel().astype(np.float64)
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-30))
+
+
+def make(dev, H=2, N=4096, CQ=32, frac=0.05, seed=0, temp=4.0, **kw):
+    from token2tile_amd.deploy_step import MaskedStepDeploy
+    from token2tile_amd.synth import generate_np
+    q, k, v = generate_np(H, N, grid=(4, 32, 32), seed=seed)
+    # sharper attention than the 1/sqrt(d)-scaled default makes the sparse
+    # structure matter for the comparison
+    q = (q.astype(np.float32) * temp).astype(np.float16)
+    deploy = MaskedStepDeploy(H, N, CQ, s_frac=frac, device=dev, **kw)
+    return deploy, q, k, v
+
+
+def state_np(state):
+    return {k_: v_.cpu().numpy() for k_, v_ in state.items()}
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_full_call_matches_oracle(dev, dtype):
+    deploy, q, k, v = make(dev)
+    tq, tk, tv = (torch.from_numpy(a).to(dev).to(dtype).contiguous() for a in (q, k, v))
+    state = deploy.init_state(tq, tk, seed=1)
+    s0 = state_np(state)
+    out = deploy.step(tq, tk, tv, state).float().cpu().numpy()
+    torch.cuda.synchronize()
+    qf, kf, vf = (t.float().cpu().numpy() for t in (tq, tk, tv))
+    if dtype == torch.bfloat16:   # the projection consumes q, k rounded to fp16
+        pass
+    eo, st, ns_ = O.full_call(qf.astype(np.float16) if dtype == torch.float16 else qf,
+                              kf.astype(np.float16) if dtype == torch.float16 else kf,
+                              vf, s0, deploy.ns, deploy.CQ)
+    assert np.abs(out - eo).max() <= 2e-2
+    assert cos(out, eo) >= 0.999
+    # the new warm-start state
+    assert np.mean(state["cq"].cpu().numpy() != st["cq2"]) < 0.01
+    # chained: S4-S6 of the oracle on the GPU's own structure -> tighter
+    last = deploy._last
+    unip = last["unip"].cpu().numpy()
+    qperm = last["qperm"].cpu().numpy()
+    kcounts = last["counts"].cpu().numpy()
+    qcounts = last["tile_sizes"].cpu().numpy()
+    gl = deploy.gl.cpu().numpy()
+    eu, er = O.select_union(gl, kcounts, qperm, qcounts, deploy.ns)
+    assert np.array_equal(unip, eu)
+    assert np.array_equal(deploy.rowcnt.cpu().numpy(), er)
+
+
+def test_reuse_call_matches_oracle(dev):
+    deploy, q, k, v = make(dev, mask_refresh=4)
+    tq, tk, tv = (torch.from_numpy(a).to(dev) for a in (q, k, v))
+    state = deploy.init_state(tq, tk, seed=2)
+    deploy.set_cfg_call(0, key=3, step=10)
+    deploy.step(tq, tk, tv, state)
+    assert deploy.last_call_full
+    snap = deploy._cfg_hold[3]
+    # a different V and Q on the reuse call
+    rng = np.random.default_rng(5)
+    v2 = rng.normal(0, 1, v.shape).astype(np.float16)
+    q2 = (q.astype(np.float32) + 0.05 * rng.normal(0, 1, q.shape)).astype(np.float16)
+    tq2, tv2 = torch.from_numpy(q2).to(dev), torch.from_numpy(v2).to(dev)
+    deploy.set_cfg_call(1, key=3, step=10)
+    out = deploy.step(tq2, tk, tv2, state).float().cpu().numpy()
+    assert not deploy.last_call_full
+    sn = {k_: (v_.cpu().numpy() if torch.is_tensor(v_) else v_) for k_, v_ in snap.items()}
+    sn["kcounts"] = sn["counts"]
+    sn["qcounts"] = sn["tile_sizes"]
+    eo = O.reuse_call(q2, k, v2, sn)
+    assert np.abs(out - eo).max() <= 2e-2 and cos(out, eo) >= 0.999
+    # refresh due at age 4 on parity 0 -> full call
+    deploy.set_cfg_call(0, key=3, step=14)
+    deploy.step(tq, tk, tv, state)
+    assert deploy.last_call_full
+
+
+def test_pin_tail_and_determinism(dev):
+    deploy, q, k, v = make(dev, pin_tail=64)
+    tq, tk, tv = (torch.from_numpy(a).to(dev) for a in (q, k, v))
+    state = deploy.init_state(tq, tk, seed=3)
+    st2 = {k_: v_.clone() for k_, v_ in state.items()}
+    s0 = state_np(state)
+    out1 = deploy.step(tq, tk, tv, state).clone()
+    out2 = deploy.step(tq, tk, tv, st2).clone()
+    assert torch.equal(out1, out2)
+    unip = deploy._last["unip"].cpu().numpy().view(np.uint32)
+    assert np.all((unip[..., 63] >> 31) & 1)
+    eo, _, _ = O.full_call(q, k, v, s0, deploy.ns, deploy.CQ, pin_tail=64)
+    o = out1.float().cpu().numpy()
+    assert np.abs(o - eo).max() <= 2e-2 and cos(o, eo) >= 0.999
+
+
+def test_bad_inputs_raise(dev):
+    from token2tile_amd.deploy_step import MaskedStepDeploy
+    with pytest.raises(ValueError):
+        MaskedStepDeploy(2, 4096, 32, C=1024, device=dev)
+    deploy, q, k, v = make(dev)
+    tq = torch.from_numpy(q).to(dev)
+    with pytest.raises(ValueError):
+        deploy.step(tq[:, :100], tq, tq, {})
+    bad = tq.clone()
+    bad[0, 5, 5] = float("nan")
+    with pytest.raises(RuntimeError):
+        deploy.init_state(bad, tq)

@@ -1,0 +1,268 @@
+// Skinny GEMMs of the call: the rank-32 projection (S1), the centroid scores
+// (S3) and the fp64 Gram matrices of the projection fit (S0).
+//
+// Both MFMA kernels compute the transposed product (output features on the
+// MFMA row axis, tokens on the column axis) so that a lane owns one token and
+// four consecutive output features per accumulator group.
+#include "t2t_common.h"
+
+// ---------------------------------------------------------------------------
+// S1: out[n, 0:32] = fp16(x[n, 0:D] @ U[0:D, 0:32]), fp32 accumulation
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ __launch_bounds__(256) void project_kernel(const uint16_t* __restrict__ x,
+                                                      const uint16_t* __restrict__ U,
+                                                      uint16_t* __restrict__ out, int N) {
+  constexpr int KS = D / 16;
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int jl = lane & 31, hh = lane >> 5;
+  const uint16_t* Uh = U + (size_t)h * D * 32;
+  // A operand = U^T: lane supplies U[16 s + 8 hh + t][jl]
+  u32x4 ua[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    uint16_t v[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] = Uh[(size_t)(16 * s + 8 * hh + t) * 32 + jl];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) ua[s][t] = (uint32_t)v[2 * t] | ((uint32_t)v[2 * t + 1] << 16);
+  }
+  const uint16_t* xh = x + (size_t)h * N * D;
+  uint16_t* oh = out + (size_t)h * N * 32;
+  for (int r0 = (blockIdx.x * 4 + wave) * 32; r0 < N; r0 += gridDim.x * 4 * 32) {
+    const int row = r0 + jl;
+    const bool ok = row < N;
+    f32x16 acc = zero16();
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      u32x4 b = {0u, 0u, 0u, 0u};
+      if (ok) b = *(const u32x4*)(xh + (size_t)row * D + 16 * s + 8 * hh);
+      if constexpr (T::code == T2T_BF16) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t w = b[t];
+          b[t] = (uint32_t)bf2h((uint16_t)(w & 0xffff)) | ((uint32_t)bf2h((uint16_t)(w >> 16)) << 16);
+        }
+      }
+      acc = Mfma<F16T>::run(ua[s], b, acc);
+    }
+    if (ok) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        u32x2 o;
+        o[0] = (uint32_t)f2h(acc[4 * g + 0]) | ((uint32_t)f2h(acc[4 * g + 1]) << 16);
+        o[1] = (uint32_t)f2h(acc[4 * g + 2]) | ((uint32_t)f2h(acc[4 * g + 3]) << 16);
+        *(u32x2*)(oh + (size_t)row * 32 + 8 * g + 4 * hh) = o;
+      }
+    }
+  }
+}
+
+template <typename T>
+static int launch_project(const void* x, const void* U, void* out, int H, int N, int D,
+                          hipStream_t st) {
+  int gx = cdiv(N, 128);
+  if (gx > 1024) gx = 1024;
+  dim3 grid(gx, H);
+  switch (D) {
+    case 128:
+      hipLaunchKernelGGL((project_kernel<T, 128>), grid, dim3(256), 0, st, (const uint16_t*)x,
+                         (const uint16_t*)U, (uint16_t*)out, N);
+      break;
+    case 64:
+      hipLaunchKernelGGL((project_kernel<T, 64>), grid, dim3(256), 0, st, (const uint16_t*)x,
+                         (const uint16_t*)U, (uint16_t*)out, N);
+      break;
+    case 32:
+      hipLaunchKernelGGL((project_kernel<T, 32>), grid, dim3(256), 0, st, (const uint16_t*)x,
+                         (const uint16_t*)U, (uint16_t*)out, N);
+      break;
+    default:
+      t2t_set_error("project: D=%d not in {32, 64, 128}", D);
+      return T2T_ERR_UNSUPPORTED;
+  }
+  T2T_LAUNCH_CHECK("project");
+  return T2T_OK;
+}
+
+extern "C" int t2t_project(const void* x, int x_dtype, const void* U, void* out, int H, int N,
+                           int D, int r, void* stream) {
+  T2T_REQUIRE(x && U && out, "project: null pointer");
+  T2T_REQUIRE(H > 0 && N > 0, "project: H=%d N=%d", H, N);
+  T2T_REQUIRE(r == 32, "project: rank r=%d (kernels are built for r=32)", r);
+  if (x_dtype == T2T_F16) return launch_project<F16T>(x, U, out, H, N, D, (hipStream_t)stream);
+  if (x_dtype == T2T_BF16) return launch_project<BF16T>(x, U, out, H, N, D, (hipStream_t)stream);
+  t2t_set_error("project: dtype %d", x_dtype);
+  return T2T_ERR_ARG;
+}
+
+// ---------------------------------------------------------------------------
+// S3: gl[n, c] = fp16(QU[n, :] . cks[c, :]), r = 32, 128-row x 128-centroid
+// tiles staged through LDS so every row segment is stored as 256 B.
+// The MFMA operand order here (centroids on the A side, two k-steps of 16)
+// is the single definition of the fp16 score; the fused selection kernel
+// uses score_block() below so its scores are bitwise the same.
+// ---------------------------------------------------------------------------
+#define SC_ROWS 128
+#define SC_CENT 128
+#define SC_PITCH (SC_CENT + 8)
+
+// A operand fragments of 32 centroids from an LDS tile [cent][32] (pitch 32)
+__device__ inline void load_cent_frag(const uint16_t* sC, int cblk, int lane, u32x4& a0, u32x4& a1) {
+  const int jl = lane & 31, hh = lane >> 5;
+  const uint16_t* p = sC + (cblk * 32 + jl) * 32 + 8 * hh;
+  a0 = *(const u32x4*)(p);
+  a1 = *(const u32x4*)(p + 16);
+}
+
+__global__ __launch_bounds__(256) void score_kernel(const uint16_t* __restrict__ QU,
+                                                    const uint16_t* __restrict__ cks,
+                                                    uint16_t* __restrict__ gl, int N, int CK) {
+  __shared__ __attribute__((aligned(16))) uint16_t sC[SC_CENT * 32];
+  __shared__ __attribute__((aligned(16))) uint16_t sO[SC_ROWS * SC_PITCH];
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int jl = lane & 31, hh = lane >> 5;
+  const int r0 = blockIdx.x * SC_ROWS;
+  const int row = r0 + wave * 32 + jl;
+  const bool ok = row < N;
+  const uint16_t* qh = QU + (size_t)h * N * 32;
+  u32x4 b0 = {0u, 0u, 0u, 0u}, b1 = {0u, 0u, 0u, 0u};
+  if (ok) {
+    b0 = *(const u32x4*)(qh + (size_t)row * 32 + 8 * hh);
+    b1 = *(const u32x4*)(qh + (size_t)row * 32 + 16 + 8 * hh);
+  }
+  const uint16_t* ch = cks + (size_t)h * CK * 32;
+  uint16_t* gh = gl + (size_t)h * N * CK;
+  for (int c0 = 0; c0 < CK; c0 += SC_CENT) {
+    __syncthreads();
+    // stage 128 centroids x 32 dims (8 KB): 512 vectors of 16 B
+    for (int i = tid; i < SC_CENT * 4; i += 256)
+      ((u32x4*)sC)[i] = ((const u32x4*)(ch + (size_t)c0 * 32))[i];
+    __syncthreads();
+#pragma unroll
+    for (int cb = 0; cb < SC_CENT / 32; ++cb) {
+      u32x4 a0, a1;
+      load_cent_frag(sC, cb, lane, a0, a1);
+      f32x16 acc = zero16();
+      acc = Mfma<F16T>::run(a0, b0, acc);
+      acc = Mfma<F16T>::run(a1, b1, acc);
+      // lane holds centroids cb*32 + 8*(a/4) + 4*hh + a%4 of token wave*32 + jl
+      uint16_t* orow = sO + (wave * 32 + jl) * SC_PITCH + cb * 32 + 4 * hh;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        u32x2 o;
+        o[0] = (uint32_t)f2h(acc[4 * g + 0]) | ((uint32_t)f2h(acc[4 * g + 1]) << 16);
+        o[1] = (uint32_t)f2h(acc[4 * g + 2]) | ((uint32_t)f2h(acc[4 * g + 3]) << 16);
+        *(u32x2*)(orow + 8 * g) = o;
+      }
+    }
+    __syncthreads();
+    // store 128 rows x 256 B
+    for (int i = tid; i < SC_ROWS * (SC_CENT / 8); i += 256) {
+      const int rr = i / (SC_CENT / 8), cc = i % (SC_CENT / 8);
+      const int grow = r0 + rr;
+      if (grow < N)
+        __builtin_nontemporal_store(*(const u32x4*)(sO + rr * SC_PITCH + cc * 8),
+                                    (u32x4*)(gh + (size_t)grow * CK + c0 + cc * 8));
+    }
+  }
+}
+
+extern "C" int t2t_score(const void* QU, const void* cks, void* gl, int H, int N, int CK, int r,
+                         void* stream) {
+  T2T_REQUIRE(QU && cks && gl, "score: null pointer");
+  T2T_REQUIRE(H > 0 && N > 0, "score: H=%d N=%d", H, N);
+  T2T_REQUIRE(r == 32, "score: r=%d (kernels are built for r=32)", r);
+  T2T_REQUIRE(CK > 0 && CK % SC_CENT == 0, "score: CK=%d must be a multiple of %d", CK, SC_CENT);
+  hipLaunchKernelGGL(score_kernel, dim3(cdiv(N, SC_ROWS), H), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)QU, (const uint16_t*)cks, (uint16_t*)gl, N, CK);
+  T2T_LAUNCH_CHECK("score");
+  return T2T_OK;
+}
+
+// ---------------------------------------------------------------------------
+// S0: G = x^T x / N in fp64 (products of fp16 values are exact in fp64; the
+// sum runs over rows in order, so the result is deterministic).
+// grid (tiles, H); each work-group owns a 64 x 64 output tile.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void gram_kernel(const uint16_t* __restrict__ x,
+                                                   double* __restrict__ G, int N, int D) {
+  __shared__ float sA[64][65];
+  __shared__ float sB[64][65];
+  const int h = blockIdx.y;
+  const int tiles = (D + 63) / 64;
+  const int ti = blockIdx.x / tiles, tj = blockIdx.x % tiles;
+  const int tid = threadIdx.x;
+  const int oi = (tid / 16) * 4, oj = (tid % 16) * 4;  // 4 x 4 outputs per thread
+  double acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = 0.0;
+  const uint16_t* xh = x + (size_t)h * N * D;
+  for (int n0 = 0; n0 < N; n0 += 64) {
+    __syncthreads();
+    for (int i = tid; i < 64 * 64; i += 256) {
+      const int rr = i / 64, cc = i % 64;
+      const int n = n0 + rr;
+      float va = 0.f, vb = 0.f;
+      if (n < N) {
+        const int ca = ti * 64 + cc, cb = tj * 64 + cc;
+        if (ca < D) {
+          uint16_t u = xh[(size_t)n * D + ca];
+          va = (T::code == T2T_BF16) ? h2f(bf2h(u)) : h2f(u);
+        }
+        if (cb < D) {
+          uint16_t u = xh[(size_t)n * D + cb];
+          vb = (T::code == T2T_BF16) ? h2f(bf2h(u)) : h2f(u);
+        }
+      }
+      sA[rr][cc] = va;
+      sB[rr][cc] = vb;
+    }
+    __syncthreads();
+    const int nr = (N - n0) < 64 ? (N - n0) : 64;
+    for (int rr = 0; rr < nr; ++rr) {
+      double a[4], b[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        a[t] = (double)sA[rr][oi + t];
+        b[t] = (double)sB[rr][oj + t];
+      }
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[p][q] = __fma_rn(a[p], b[q], acc[p][q]);
+    }
+  }
+  const double inv = 1.0 / (double)N;
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = ti * 64 + oi + p, j = tj * 64 + oj + q;
+      if (i < D && j < D) G[((size_t)h * D + i) * D + j] = acc[p][q] * inv;
+    }
+}
+
+extern "C" int t2t_gram(const void* x, int x_dtype, double* G, int H, int N, int D, void* stream) {
+  T2T_REQUIRE(x && G, "gram: null pointer");
+  T2T_REQUIRE(H > 0 && N > 0 && D > 0 && D <= 128, "gram: H=%d N=%d D=%d", H, N, D);
+  const int tiles = (D + 63) / 64;
+  dim3 grid(tiles * tiles, H);
+  if (x_dtype == T2T_F16)
+    hipLaunchKernelGGL(gram_kernel<F16T>, grid, dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)x, G, N, D);
+  else if (x_dtype == T2T_BF16)
+    hipLaunchKernelGGL(gram_kernel<BF16T>, grid, dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)x, G, N, D);
+  else {
+    t2t_set_error("gram: dtype %d", x_dtype);
+    return T2T_ERR_ARG;
+  }
+  T2T_LAUNCH_CHECK("gram");
+  return T2T_OK;
+}

@@ -1,0 +1,643 @@
+// S2: warm-started k-means maintenance, and the init_state helpers
+// (fast_assign, deterministic centroid update), for gfx950.
+//
+// Pipeline of one maintenance call (all deterministic):
+//   prep centroids -> assign (MFMA distances + argmin) -> stable counting
+//   sort of the labels (chunk histograms, column scans, ballot-ranked
+//   scatter) -> per-cluster sums by one owner wave per cluster, in sorted
+//   row order (exact int64 fixed point for query clusters; sequential fp32
+//   for key clusters, which also writes the cluster-ordered V) -> value
+//   statistics (lam, sumv).
+#include "t2t_common.h"
+
+#define KM_R 32            // rank of the projected space
+#define AS_CHUNK 256       // centroids staged per LDS chunk in assign
+#define SORT_CH 1024       // rows per counting-sort chunk
+#define KM_MAXC 4096
+
+static inline int pad32(int c) { return (c + 31) & ~31; }
+
+// ---------------------------------------------------------------------------
+// assignment.  Transposed MFMA product: centroids on the row axis (A), tokens
+// on the column axis (B), so a lane owns one token and 16 centroids per
+// 32-centroid block, visited in ascending index order.
+//   MODE 0 (kmeans):     d = cnorm + x.(-2c), argmin, ties -> lowest index
+//   MODE 1 (fast_assign): d2 = |x|^2 + (cn2 - 2 x.c); key = (bits(d2) & ~m) | c
+// ---------------------------------------------------------------------------
+template <int MODE, int D>
+__global__ __launch_bounds__(256) void assign_kernel(const uint16_t* __restrict__ X,
+                                                     const uint16_t* __restrict__ cen,
+                                                     int32_t* __restrict__ labels, int N, int C,
+                                                     int pin_begin, int pin_label, int ibits) {
+  constexpr int KS = D / 16;
+  __shared__ __attribute__((aligned(16))) uint16_t sC[AS_CHUNK * D];
+  __shared__ float sN[AS_CHUNK];
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int jl = lane & 31, hh = lane >> 5;
+  const int row = blockIdx.x * 128 + wave * 32 + jl;
+  const bool ok = row < N;
+  const uint16_t* xh = X + (size_t)h * N * D;
+  u32x4 bx[KS];
+  float xsq = 0.f;
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    bx[s] = u32x4{0u, 0u, 0u, 0u};
+    if (ok) bx[s] = *(const u32x4*)(xh + (size_t)row * D + 16 * s + 8 * hh);
+    if (MODE == 1) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float a = h2f((uint16_t)(bx[s][t] & 0xffff)), b = h2f((uint16_t)(bx[s][t] >> 16));
+        xsq += a * a + b * b;
+      }
+    }
+  }
+  if (MODE == 1) xsq += __shfl_xor(xsq, 32, 64);
+  const uint16_t* ch = cen + (size_t)h * C * D;
+  const int Cp = (C + 31) & ~31;
+  float best = __builtin_inff();
+  int bidx = 0;
+  int bkey = 0x7fffffff;
+  const int kmask = -(1 << ibits);
+  for (int c0 = 0; c0 < Cp; c0 += AS_CHUNK) {
+    const int nc = (Cp - c0) < AS_CHUNK ? (Cp - c0) : AS_CHUNK;
+    __syncthreads();
+    // stage the chunk: -2c (MODE 0, exact in fp16) or c (MODE 1); padding = 0
+    for (int i = tid; i < nc * D / 8; i += 256) {
+      const int ci = c0 + (i * 8) / D;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (ci < C) v = ((const u32x4*)(ch + (size_t)c0 * D))[i];
+      if (MODE == 0) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          v[t] = (uint32_t)f2h(-2.0f * h2f((uint16_t)(v[t] & 0xffff))) |
+                 ((uint32_t)f2h(-2.0f * h2f((uint16_t)(v[t] >> 16))) << 16);
+      }
+      ((u32x4*)sC)[i] = v;
+    }
+    // squared norms in fp32, sequential over the dims (each square is exact)
+    for (int i = tid; i < nc; i += 256) {
+      const int ci = c0 + i;
+      float s = 0.f;
+      if (ci < C) {
+        const uint16_t* cp = ch + (size_t)ci * D;
+        for (int d = 0; d < D; ++d) {
+          const float v = h2f(cp[d]);
+          s = s + v * v;
+        }
+      }
+      sN[i] = (ci < C) ? s : __builtin_inff();
+    }
+    __syncthreads();
+    for (int cb = 0; cb < nc / 32; ++cb) {
+      f32x16 acc;
+#pragma unroll
+      for (int a = 0; a < 16; ++a)
+        acc[a] = (MODE == 0) ? sN[cb * 32 + 8 * (a / 4) + 4 * hh + (a % 4)] : 0.f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4 av = *(const u32x4*)(sC + (cb * 32 + jl) * D + 16 * s + 8 * hh);
+        acc = Mfma<F16T>::run(av, bx[s], acc);
+      }
+#pragma unroll
+      for (int a = 0; a < 16; ++a) {
+        const int ci = c0 + cb * 32 + 8 * (a / 4) + 4 * hh + (a % 4);
+        if (MODE == 0) {
+          if (acc[a] < best) {
+            best = acc[a];
+            bidx = ci;
+          }
+        } else {
+          const float cn2 = sN[cb * 32 + 8 * (a / 4) + 4 * hh + (a % 4)];
+          const float d2 = xsq + (cn2 - 2.0f * acc[a]);
+          int key = (__builtin_bit_cast(int, d2) & kmask) | ci;
+          if (ci >= C) key = 0x7fffffff;
+          bkey = key < bkey ? key : bkey;
+        }
+      }
+    }
+  }
+  int lab;
+  if (MODE == 0) {
+    const float ob = __shfl_xor(best, 32, 64);
+    const int oi = __shfl_xor(bidx, 32, 64);
+    if (ob < best || (ob == best && oi < bidx)) {
+      best = ob;
+      bidx = oi;
+    }
+    lab = bidx;
+  } else {
+    const int ok2 = __shfl_xor(bkey, 32, 64);
+    bkey = ok2 < bkey ? ok2 : bkey;
+    lab = bkey & ((1 << ibits) - 1);
+  }
+  if (ok && hh == 0) {
+    if (row >= pin_begin) lab = pin_label;
+    labels[(size_t)h * N + row] = lab;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// stable counting sort of labels -> counts, cbase (exclusive scan), perm
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void sort_hist_kernel(const int32_t* __restrict__ lab,
+                                                        int32_t* __restrict__ chist, int N, int C,
+                                                        int nChunk) {
+  __shared__ int hist[KM_MAXC];
+  const int h = blockIdx.y, k = blockIdx.x, tid = threadIdx.x;
+  for (int i = tid; i < C; i += 256) hist[i] = 0;
+  __syncthreads();
+  const int r0 = k * SORT_CH;
+  const int r1 = (r0 + SORT_CH) < N ? (r0 + SORT_CH) : N;
+  for (int r = r0 + tid; r < r1; r += 256) atomicAdd(&hist[lab[(size_t)h * N + r]], 1);
+  __syncthreads();
+  int32_t* out = chist + ((size_t)h * nChunk + k) * C;
+  for (int i = tid; i < C; i += 256) out[i] = hist[i];
+}
+
+__global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* __restrict__ chist,
+                                                         int32_t* __restrict__ counts,
+                                                         int32_t* __restrict__ cbase, int C,
+                                                         int nChunk) {
+  __shared__ int wsum[16];
+  __shared__ int sbase[KM_MAXC];
+  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int32_t* ch = chist + (size_t)h * nChunk * C;
+  // column scans over chunks: chunk-local start offsets, and totals
+  for (int c = tid; c < C; c += 1024) {
+    int run = 0;
+    for (int k = 0; k < nChunk; ++k) {
+      const int v = ch[(size_t)k * C + c];
+      ch[(size_t)k * C + c] = run;
+      run += v;
+    }
+    sbase[c] = run;
+    counts[(size_t)h * C + c] = run;
+  }
+  __syncthreads();
+  // exclusive scan of the totals over clusters (4 per thread, in order)
+  const int per = (C + 1023) / 1024;
+  int loc = 0;
+  for (int i = 0; i < per; ++i) {
+    const int c = tid * per + i;
+    if (c < C) loc += sbase[c];
+  }
+  const int inc = wave_incl_scan(loc);
+  if (lane == 63) wsum[w] = inc;
+  __syncthreads();
+  int add = 0;
+  for (int i = 0; i < w; ++i) add += wsum[i];
+  int run = add + inc - loc;
+  __syncthreads();
+  for (int i = 0; i < per; ++i) {
+    const int c = tid * per + i;
+    if (c < C) {
+      const int v = sbase[c];
+      sbase[c] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  for (int c = tid; c < C; c += 1024) {
+    const int b = sbase[c];
+    cbase[(size_t)h * C + c] = b;
+    for (int k = 0; k < nChunk; ++k) ch[(size_t)k * C + c] += b;
+  }
+}
+
+__device__ inline void wave_sync_km() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// one wave per chunk; rows of equal label keep their order (ballot ranking)
+__global__ __launch_bounds__(64) void sort_scatter_kernel(const int32_t* __restrict__ lab,
+                                                          const int32_t* __restrict__ chist,
+                                                          int32_t* __restrict__ perm, int N, int C,
+                                                          int nChunk, int lbits) {
+  __shared__ int cc[KM_MAXC];
+  const int h = blockIdx.y, k = blockIdx.x, l = threadIdx.x;
+  const int32_t* off = chist + ((size_t)h * nChunk + k) * C;
+  for (int i = l; i < C; i += 64) cc[i] = off[i];
+  wave_sync_km();
+  const int r0 = k * SORT_CH;
+  const int r1 = (r0 + SORT_CH) < N ? (r0 + SORT_CH) : N;
+  const unsigned long long lt = (1ull << l) - 1ull;
+  for (int r = r0; r < r1; r += 64) {
+    const int row = r + l;
+    const bool valid = row < r1;
+    const int c = valid ? lab[(size_t)h * N + row] : 0;
+    unsigned long long peers = __ballot(valid);
+    for (int b = 0; b < lbits; ++b) {
+      const unsigned long long bb = __ballot((c >> b) & 1);
+      peers &= ((c >> b) & 1) ? bb : ~bb;
+    }
+    const int rank = __popcll(peers & lt);
+    const int leader = (int)__ffsll((long long)peers) - 1;
+    int base = 0;
+    if (valid && l == leader) {
+      base = cc[c];
+      cc[c] = base + __popcll(peers);
+    }
+    base = __shfl(base, leader < 0 ? 0 : leader, 64);
+    if (valid) perm[(size_t)h * N + base + rank] = row;
+    wave_sync_km();
+  }
+}
+
+struct SortBufs {
+  int32_t* chist;  // [H, nChunk, C]
+};
+
+static int run_sort(const int32_t* lab, int32_t* counts, int32_t* cbase, int32_t* perm,
+                    int32_t* chist, int H, int N, int C, hipStream_t st) {
+  const int nChunk = cdiv(N, SORT_CH);
+  int lbits = 1;
+  while ((1 << lbits) < C) ++lbits;
+  hipLaunchKernelGGL(sort_hist_kernel, dim3(nChunk, H), dim3(256), 0, st, lab, chist, N, C, nChunk);
+  hipLaunchKernelGGL(sort_scan_kernel, dim3(H), dim3(1024), 0, st, chist, counts, cbase, C, nChunk);
+  hipLaunchKernelGGL(sort_scatter_kernel, dim3(nChunk, H), dim3(64), 0, st, lab, chist, perm, N, C,
+                     nChunk, lbits);
+  return t2t_check_launch("counting sort");
+}
+
+// ---------------------------------------------------------------------------
+// per-cluster integer sums in sorted order -> fp16 means (one wave/cluster)
+//   MODE 0: rne(x * 32768) sums, mean = fp16(f32(S) / (32768 * f32(n)))
+//   MODE 1: rne(x * 2^20) sums, mean = fp16(f32(f64(S) / 2^20 / f64(n)))
+// empty clusters keep `old`.
+// ---------------------------------------------------------------------------
+template <int MODE>
+__global__ __launch_bounds__(256) void fixed_mean_kernel(const uint16_t* __restrict__ X,
+                                                         const int32_t* __restrict__ perm,
+                                                         const int32_t* __restrict__ counts,
+                                                         const int32_t* __restrict__ cbase,
+                                                         const uint16_t* __restrict__ old,
+                                                         uint16_t* __restrict__ out, int N, int C) {
+  const int h = blockIdx.y;
+  const int l = threadIdx.x & 63;
+  const int c = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (c >= C) return;
+  const int n = counts[(size_t)h * C + c];
+  const int b = cbase[(size_t)h * C + c];
+  const int d = l & 31, par = l >> 5;
+  const float scale = MODE == 0 ? 32768.0f : 1048576.0f;
+  long long S = 0;
+  const int32_t* ph = perm + (size_t)h * N + b;
+  const uint16_t* xh = X + (size_t)h * N * KM_R;
+  for (int i = par; i < n; i += 2) {
+    const int row = ph[i];
+    S += (long long)rintf(h2f(xh[(size_t)row * KM_R + d]) * scale);
+  }
+  S += __shfl_xor(S, 32, 64);
+  if (par == 0) {
+    const size_t o = ((size_t)h * C + c) * KM_R + d;
+    uint16_t v;
+    if (n == 0) {
+      v = old[o];
+    } else if (MODE == 0) {
+      v = f2h((float)S / (32768.0f * (float)n));
+    } else {
+      const double m = ((double)S / 1048576.0) / (double)n;
+      v = f2h((float)m);
+    }
+    out[o] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// key side: per cluster, sequential fp32 sums of KU (lanes 0..31, one dim
+// each) and V (two dims per lane) in sorted row order; V_sorted rows; ck2.
+// perm == nullptr: rows are already cluster ordered (V_sorted input).
+// ---------------------------------------------------------------------------
+#define KG_UNR 8
+template <typename T>
+__global__ __launch_bounds__(256) void key_gather_kernel(
+    const uint16_t* __restrict__ KU, const uint16_t* __restrict__ V,
+    const int32_t* __restrict__ perm, const int32_t* __restrict__ counts,
+    const int32_t* __restrict__ cbase, const uint16_t* __restrict__ ck0, float* __restrict__ ck2,
+    uint16_t* __restrict__ V_sorted, float* __restrict__ vsum, int N, int C) {
+  const int h = blockIdx.y;
+  const int l = threadIdx.x & 63;
+  const int c = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (c >= C) return;
+  const int n = counts[(size_t)h * C + c];
+  const int b = cbase[(size_t)h * C + c];
+  const int32_t* ph = perm ? perm + (size_t)h * N + b : nullptr;
+  const uint16_t* kh = KU ? KU + (size_t)h * N * KM_R : nullptr;
+  const uint32_t* vh = (const uint32_t*)(V + (size_t)h * N * 128);
+  uint32_t* vsh = V_sorted ? (uint32_t*)(V_sorted + (size_t)h * N * 128) : nullptr;
+  float ax = 0.f, v0 = 0.f, v1 = 0.f;
+  for (int i = 0; i < n; i += KG_UNR) {
+    int rw[KG_UNR];
+    uint32_t vv[KG_UNR];
+    float xv[KG_UNR];
+#pragma unroll
+    for (int u = 0; u < KG_UNR; ++u) rw[u] = (i + u < n) ? (ph ? ph[i + u] : b + i + u) : -1;
+#pragma unroll
+    for (int u = 0; u < KG_UNR; ++u) {
+      vv[u] = rw[u] >= 0 ? __builtin_nontemporal_load(&vh[(size_t)rw[u] * 64 + l]) : 0u;
+      xv[u] = (kh && rw[u] >= 0 && l < 32) ? h2f(kh[(size_t)rw[u] * KM_R + l]) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < KG_UNR; ++u) {
+      if (rw[u] < 0) break;
+      if (vsh) vsh[(size_t)(b + i + u) * 64 + l] = vv[u];
+      v0 += T::to_f((uint16_t)(vv[u] & 0xffff));
+      v1 += T::to_f((uint16_t)(vv[u] >> 16));
+      ax += xv[u];
+    }
+  }
+  float* vo = vsum + ((size_t)h * C + c) * 128 + 2 * l;
+  vo[0] = v0;
+  vo[1] = v1;
+  if (ck2 && l < 32) {
+    const size_t o = ((size_t)h * C + c) * KM_R + l;
+    ck2[o] = n ? ax / (float)n : h2f(ck0[o]);
+  }
+}
+
+// lam = max(1, max|vsum| / 32768); sumv = fp16(vsum * (1 / lam)); one block/head
+__global__ __launch_bounds__(1024) void vstats_kernel(const float* __restrict__ vsum,
+                                                      uint16_t* __restrict__ sumv,
+                                                      float* __restrict__ lam, int C) {
+  __shared__ float red[16];
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const size_t CE = (size_t)C * 128;
+  const float* vh = vsum + (size_t)h * CE;
+  float mx = 0.f;
+  for (size_t i = tid; i < CE; i += 1024) mx = fmaxf(mx, fabsf(vh[i]));
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = 0.f;
+  for (int i = 0; i < 16; ++i) mx = fmaxf(mx, red[i]);
+  const float lm = fmaxf(1.0f, mx / 32768.0f);
+  const float inv = 1.0f / lm;
+  if (tid == 0) lam[h] = lm;
+  uint16_t* sh = sumv + (size_t)h * CE;
+  for (size_t i = tid; i < CE; i += 1024) sh[i] = f2h(vh[i] * inv);
+}
+
+// ---------------------------------------------------------------------------
+// host entry points
+// ---------------------------------------------------------------------------
+struct KmmWs {
+  int32_t* qlab1;
+  uint16_t* cq1;
+  int32_t* perm1;
+  int32_t* counts1;
+  int32_t* cbase1;
+  int32_t* cbaseq;
+  int32_t* cbasek;
+  int32_t* chist;
+  float* vsum;
+  size_t total;
+};
+
+static KmmWs kmm_layout(int H, int N, int CQ, int CK, void* base) {
+  WsCarver w(base);
+  KmmWs k;
+  const int nChunk = cdiv(N, SORT_CH);
+  const int Cmax = CQ > CK ? CQ : CK;
+  k.qlab1 = w.take<int32_t>((size_t)H * N);
+  k.cq1 = w.take<uint16_t>((size_t)H * CQ * KM_R);
+  k.perm1 = w.take<int32_t>((size_t)H * N);
+  k.counts1 = w.take<int32_t>((size_t)H * CQ);
+  k.cbase1 = w.take<int32_t>((size_t)H * CQ);
+  k.cbaseq = w.take<int32_t>((size_t)H * CQ);
+  k.cbasek = w.take<int32_t>((size_t)H * CK);
+  k.chist = w.take<int32_t>((size_t)H * nChunk * Cmax);
+  k.vsum = w.take<float>((size_t)H * CK * 128);
+  k.total = w.off;
+  return k;
+}
+
+extern "C" size_t t2t_kmm_ws_bytes(int H, int N, int CQ, int CK) {
+  return kmm_layout(H, N, CQ, CK, nullptr).total;
+}
+
+static int launch_assign_km(const void* X, const void* cen, int32_t* lab, int H, int N, int C,
+                            int pin_begin, int pin_label, hipStream_t st) {
+  hipLaunchKernelGGL((assign_kernel<0, KM_R>), dim3(cdiv(N, 128), H), dim3(256), 0, st,
+                     (const uint16_t*)X, (const uint16_t*)cen, lab, N, C, pin_begin, pin_label, 0);
+  return t2t_check_launch("assign");
+}
+
+template <typename T>
+static void launch_key_gather(const void* KU, const void* V, const int32_t* perm,
+                              const int32_t* counts, const int32_t* cbase, const void* ck0,
+                              float* ck2, void* V_sorted, float* vsum, int H, int N, int C,
+                              hipStream_t st) {
+  hipLaunchKernelGGL(key_gather_kernel<T>, dim3(cdiv(C, 4), H), dim3(256), 0, st,
+                     (const uint16_t*)KU, (const uint16_t*)V, perm, counts, cbase,
+                     (const uint16_t*)ck0, ck2, (uint16_t*)V_sorted, vsum, N, C);
+}
+
+#define KM_CHECK(x)            \
+  do {                         \
+    int _rc = (x);             \
+    if (_rc) return _rc;       \
+  } while (0)
+
+extern "C" int t2t_kmm_run(const void* QU, const void* KU, const void* V, int v_dtype,
+                           const void* cq0, const void* ck0, int32_t* qlab, void* cq2,
+                           int32_t* klab, float* ck2, int32_t* qcounts, int32_t* qperm,
+                           int32_t* kcounts, int32_t* kperm, void* V_sorted, void* sumv,
+                           float* lam, int H, int N, int CQ, int CK, int pin_tail, void* ws,
+                           size_t ws_bytes, void* stream) {
+  T2T_REQUIRE(QU && KU && V && cq0 && ck0 && qlab && cq2 && klab && ck2 && qcounts && qperm &&
+                  kcounts && kperm && V_sorted && sumv && lam,
+              "kmm_run: null pointer");
+  T2T_REQUIRE(v_dtype == T2T_F16 || v_dtype == T2T_BF16, "kmm_run: dtype %d", v_dtype);
+  T2T_REQUIRE(H > 0 && N > 0, "kmm_run: H=%d N=%d", H, N);
+  T2T_REQUIRE(CQ >= 1 && CQ <= KM_MAXC && CK >= 1 && CK <= KM_MAXC,
+              "kmm_run: CQ=%d CK=%d must be in [1, %d]", CQ, CK, KM_MAXC);
+  T2T_REQUIRE(pin_tail >= 0 && pin_tail <= N, "kmm_run: pin_tail must be in [0, N]");
+  const KmmWs need = kmm_layout(H, N, CQ, CK, nullptr);
+  if (!ws || ws_bytes < need.total) {
+    t2t_set_error("kmm_run: workspace %zu < %zu bytes", ws_bytes, need.total);
+    return T2T_ERR_WORKSPACE;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  KmmWs w = kmm_layout(H, N, CQ, CK, ws);
+  const int nores = N + 1;  // no pinned rows
+  // query pass 1
+  KM_CHECK(launch_assign_km(QU, cq0, w.qlab1, H, N, CQ, nores, 0, st));
+  KM_CHECK(run_sort(w.qlab1, w.counts1, w.cbase1, w.perm1, w.chist, H, N, CQ, st));
+  hipLaunchKernelGGL(fixed_mean_kernel<0>, dim3(cdiv(CQ, 4), H), dim3(256), 0, st,
+                     (const uint16_t*)QU, w.perm1, w.counts1, w.cbase1, (const uint16_t*)cq0,
+                     w.cq1, N, CQ);
+  T2T_LAUNCH_CHECK("qmean 1");
+  // query pass 2
+  KM_CHECK(launch_assign_km(QU, w.cq1, qlab, H, N, CQ, nores, 0, st));
+  KM_CHECK(run_sort(qlab, qcounts, w.cbaseq, qperm, w.chist, H, N, CQ, st));
+  hipLaunchKernelGGL(fixed_mean_kernel<0>, dim3(cdiv(CQ, 4), H), dim3(256), 0, st,
+                     (const uint16_t*)QU, qperm, qcounts, w.cbaseq, (const uint16_t*)w.cq1,
+                     (uint16_t*)cq2, N, CQ);
+  T2T_LAUNCH_CHECK("qmean 2");
+  // key pass
+  KM_CHECK(launch_assign_km(KU, ck0, klab, H, N, CK, pin_tail > 0 ? N - pin_tail : nores,
+                            CK - 1, st));
+  KM_CHECK(run_sort(klab, kcounts, w.cbasek, kperm, w.chist, H, N, CK, st));
+  if (v_dtype == T2T_F16)
+    launch_key_gather<F16T>(KU, V, kperm, kcounts, w.cbasek, ck0, ck2, V_sorted, w.vsum, H, N, CK,
+                            st);
+  else
+    launch_key_gather<BF16T>(KU, V, kperm, kcounts, w.cbasek, ck0, ck2, V_sorted, w.vsum, H, N, CK,
+                             st);
+  T2T_LAUNCH_CHECK("key gather");
+  hipLaunchKernelGGL(vstats_kernel, dim3(H), dim3(1024), 0, st, w.vsum, (uint16_t*)sumv, lam, CK);
+  T2T_LAUNCH_CHECK("vstats");
+  return T2T_OK;
+}
+
+// ---- value statistics of a reuse call ----
+__global__ __launch_bounds__(1024) void cbase_kernel(const int32_t* __restrict__ counts,
+                                                     int32_t* __restrict__ cbase, int C) {
+  __shared__ int wsum[16];
+  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int per = (C + 1023) / 1024;
+  int loc = 0;
+  for (int i = 0; i < per; ++i) {
+    const int c = tid * per + i;
+    if (c < C) loc += counts[(size_t)h * C + c];
+  }
+  const int inc = wave_incl_scan(loc);
+  if (lane == 63) wsum[w] = inc;
+  __syncthreads();
+  int run = inc - loc;
+  for (int i = 0; i < w; ++i) run += wsum[i];
+  for (int i = 0; i < per; ++i) {
+    const int c = tid * per + i;
+    if (c < C) {
+      cbase[(size_t)h * C + c] = run;
+      run += counts[(size_t)h * C + c];
+    }
+  }
+}
+
+struct VWs {
+  int32_t* cbase;
+  float* vsum;
+  size_t total;
+};
+static VWs vws_layout(int H, int CK, void* base) {
+  WsCarver w(base);
+  VWs v;
+  v.cbase = w.take<int32_t>((size_t)H * CK);
+  v.vsum = w.take<float>((size_t)H * CK * 128);
+  v.total = w.off;
+  return v;
+}
+
+extern "C" size_t t2t_vstats_ws_bytes(int H, int N, int CK) {
+  (void)N;
+  return vws_layout(H, CK, nullptr).total;
+}
+
+static int vstats_common(const void* V, int v_dtype, const int32_t* kperm, const int32_t* kcounts,
+                         void* V_sorted, void* sumv, float* lam, int H, int N, int CK, void* ws,
+                         size_t ws_bytes, hipStream_t st) {
+  T2T_REQUIRE(V && kcounts && sumv && lam, "vstats: null pointer");
+  T2T_REQUIRE(v_dtype == T2T_F16 || v_dtype == T2T_BF16, "vstats: dtype %d", v_dtype);
+  T2T_REQUIRE(H > 0 && N > 0 && CK >= 1 && CK <= KM_MAXC, "vstats: H=%d N=%d CK=%d", H, N, CK);
+  const size_t need = vws_layout(H, CK, nullptr).total;
+  if (!ws || ws_bytes < need) {
+    t2t_set_error("vstats: workspace %zu < %zu bytes", ws_bytes, need);
+    return T2T_ERR_WORKSPACE;
+  }
+  VWs w = vws_layout(H, CK, ws);
+  hipLaunchKernelGGL(cbase_kernel, dim3(H), dim3(1024), 0, st, kcounts, w.cbase, CK);
+  if (v_dtype == T2T_F16)
+    launch_key_gather<F16T>(nullptr, V, kperm, kcounts, w.cbase, nullptr, nullptr, V_sorted,
+                            w.vsum, H, N, CK, st);
+  else
+    launch_key_gather<BF16T>(nullptr, V, kperm, kcounts, w.cbase, nullptr, nullptr, V_sorted,
+                             w.vsum, H, N, CK, st);
+  hipLaunchKernelGGL(vstats_kernel, dim3(H), dim3(1024), 0, st, w.vsum, (uint16_t*)sumv, lam, CK);
+  T2T_LAUNCH_CHECK("vstats");
+  return T2T_OK;
+}
+
+extern "C" int t2t_kmm_run_vstats_gather(const void* V, int v_dtype, const int32_t* kperm,
+                                         const int32_t* kcounts, void* V_sorted, void* sumv,
+                                         float* lam, int H, int N, int CK, void* ws,
+                                         size_t ws_bytes, void* stream) {
+  T2T_REQUIRE(kperm && V_sorted, "vstats_gather: null kperm / V_sorted");
+  return vstats_common(V, v_dtype, kperm, kcounts, V_sorted, sumv, lam, H, N, CK, ws, ws_bytes,
+                       (hipStream_t)stream);
+}
+
+extern "C" int t2t_kmm_run_vstats(const void* V_sorted, int v_dtype, const int32_t* kcounts,
+                                  void* sumv, float* lam, int H, int N, int CK, void* ws,
+                                  size_t ws_bytes, void* stream) {
+  return vstats_common(V_sorted, v_dtype, nullptr, kcounts, nullptr, sumv, lam, H, N, CK, ws,
+                       ws_bytes, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// init_state helpers
+// ---------------------------------------------------------------------------
+extern "C" int t2t_fast_assign(const void* x, const void* c, int32_t* labels, int H, int N, int C,
+                               int D, void* stream) {
+  T2T_REQUIRE(x && c && labels, "fast_assign: null pointer");
+  T2T_REQUIRE(H > 0 && N > 0 && C >= 1 && C <= KM_MAXC, "fast_assign: H=%d N=%d C=%d", H, N, C);
+  T2T_REQUIRE(D == 32 || D == 64 || D == 128, "fast_assign: D=%d not in {32, 64, 128}", D);
+  hipStream_t st = (hipStream_t)stream;
+  int ibits = 1;
+  while ((1 << ibits) < C) ++ibits;
+  const dim3 g(cdiv(N, 128), H);
+  if (D == 32)
+    hipLaunchKernelGGL((assign_kernel<1, 32>), g, dim3(256), 0, st, (const uint16_t*)x,
+                       (const uint16_t*)c, labels, N, C, N + 1, 0, ibits);
+  else if (D == 64)
+    hipLaunchKernelGGL((assign_kernel<1, 64>), g, dim3(256), 0, st, (const uint16_t*)x,
+                       (const uint16_t*)c, labels, N, C, N + 1, 0, ibits);
+  else
+    hipLaunchKernelGGL((assign_kernel<1, 128>), g, dim3(256), 0, st, (const uint16_t*)x,
+                       (const uint16_t*)c, labels, N, C, N + 1, 0, ibits);
+  T2T_LAUNCH_CHECK("fast_assign");
+  return T2T_OK;
+}
+
+struct DetWs {
+  int32_t* perm;
+  int32_t* cbase;
+  int32_t* chist;
+  size_t total;
+};
+static DetWs det_layout(int H, int N, int C, void* base) {
+  WsCarver w(base);
+  DetWs d;
+  d.perm = w.take<int32_t>((size_t)H * N);
+  d.cbase = w.take<int32_t>((size_t)H * C);
+  d.chist = w.take<int32_t>((size_t)H * cdiv(N, SORT_CH) * C);
+  d.total = w.off;
+  return d;
+}
+
+extern "C" size_t t2t_det_update_ws_bytes(int H, int N, int C) {
+  return det_layout(H, N, C, nullptr).total;
+}
+
+extern "C" int t2t_det_centroid_update(const void* x, const int32_t* labels, const void* old,
+                                       void* out, int32_t* counts, int H, int N, int C, int D,
+                                       void* ws, size_t ws_bytes, void* stream) {
+  T2T_REQUIRE(x && labels && old && out && counts, "det_update: null pointer");
+  T2T_REQUIRE(H > 0 && N > 0 && C >= 1 && C <= KM_MAXC, "det_update: H=%d N=%d C=%d", H, N, C);
+  T2T_REQUIRE(D == KM_R, "det_update: D=%d (built for %d)", D, KM_R);
+  const size_t need = det_layout(H, N, C, nullptr).total;
+  if (!ws || ws_bytes < need) {
+    t2t_set_error("det_update: workspace %zu < %zu bytes", ws_bytes, need);
+    return T2T_ERR_WORKSPACE;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  DetWs w = det_layout(H, N, C, ws);
+  KM_CHECK(run_sort(labels, counts, w.cbase, w.perm, w.chist, H, N, C, st));
+  hipLaunchKernelGGL(fixed_mean_kernel<1>, dim3(cdiv(C, 4), H), dim3(256), 0, st,
+                     (const uint16_t*)x, w.perm, counts, w.cbase, (const uint16_t*)old,
+                     (uint16_t*)out, N, C);
+  T2T_LAUNCH_CHECK("det_update");
+  return T2T_OK;
+}

@@ -1,0 +1,319 @@
+// S4: per-query key-cluster selection and query-cluster union (gfx950).
+//
+// One wave owns a run of consecutive SORTED query rows (qperm order), so the
+// work is balanced whatever the query-cluster sizes are.  For each row the
+// 2048 fp16 scores sit in registers (lane l holds clusters 512 g + 8 l + j,
+// g < 4, j < 8), and the budget threshold is found exactly with two 8-bit
+// radix passes over a wave-private, size-weighted LDS histogram:
+//   pass 1: high byte of the ordered key, pass 2: low byte inside the
+//   crossing high-byte bin.
+// Ties at the threshold are resolved in ascending cluster order with wave
+// prefix sums.  Each lane keeps the OR of its 32 selection bits across the
+// rows of one query cluster and flushes them with one atomicOr per word when
+// the run crosses into the next cluster, so the union needs no partial
+// buffers.
+#include "t2t_common.h"
+
+#define SEL_NC 2048
+#define SEL_WAVES 4
+#define SEL_ROWS_PER_WAVE 16
+
+__device__ inline void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// off[h, 0..CQ] = exclusive scan of qcounts (off[CQ] = total rows); zero unip
+__global__ __launch_bounds__(1024) void select_prep_kernel(const int32_t* __restrict__ qcounts,
+                                                           int32_t* __restrict__ off,
+                                                           int32_t* __restrict__ unip, int CQ) {
+  __shared__ int wsum[16];
+  __shared__ int carry;
+  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  if (tid == 0) carry = 0;
+  __syncthreads();
+  for (int c0 = 0; c0 < CQ; c0 += 1024) {
+    const int c = c0 + tid;
+    const int v = c < CQ ? qcounts[(size_t)h * CQ + c] : 0;
+    const int inc = wave_incl_scan(v);
+    if (lane == 63) wsum[w] = inc;
+    __syncthreads();
+    int add = carry;
+    for (int i = 0; i < w; ++i) add += wsum[i];
+    if (c < CQ) off[(size_t)h * (CQ + 1) + c] = add + inc - v;
+    __syncthreads();
+    if (tid == 1023) carry = add + inc;
+    __syncthreads();
+  }
+  if (tid == 0) off[(size_t)h * (CQ + 1) + CQ] = carry;
+  int32_t* u = unip + (size_t)h * CQ * (SEL_NC / 32);
+  for (int i = tid; i < CQ * (SEL_NC / 32); i += 1024) u[i] = 0;
+}
+
+// Find the bin where the running (descending) weight first reaches ns.
+// hist has 256 bins, bin 255 = largest keys.  Lane l scans bins 255-4l..252-4l.
+// Returns the bin; *above = weight of all higher bins; *inbin = its weight.
+__device__ inline int find_cross(const int* hist, int base, int ns, int* above, int* inbin) {
+  const int l = __lane_id();
+  int w[4];
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[i] = hist[255 - 4 * l - i];
+    s += w[i];
+  }
+  const int inc = wave_incl_scan(s);
+  const int ex = inc - s + base;
+  const bool mine = (ex < ns) && (ex + s >= ns);
+  int bin = 0, ab = 0, ib = 0;
+  if (mine) {
+    int cum = ex;
+    bool done = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (!done && cum + w[i] >= ns) {
+        bin = 255 - 4 * l - i;
+        ab = cum;
+        ib = w[i];
+        done = true;
+      }
+      cum += w[i];
+    }
+  }
+  const unsigned long long bal = __ballot(mine);
+  const int src = bal ? (int)__ffsll((long long)bal) - 1 : 0;
+  *above = __shfl(ab, src, 64);
+  *inbin = __shfl(ib, src, 64);
+  return __shfl(bin, src, 64);
+}
+
+// Selection of one row.  keys/sz: the lane's 32 clusters (index 8 g + j).
+// Returns the lane's 32 selection bits; *rowcnt = selected keys (all lanes).
+__device__ inline uint32_t select_row(const int (&key)[32], const int (&sz)[32], int* hist, int ns,
+                                      int* rowcnt) {
+  const int l = __lane_id();
+  // ---- pass 1: high byte ----
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hist[4 * l + i] = 0;
+  wave_sync();
+#pragma unroll
+  for (int i = 0; i < 32; ++i)
+    if (sz[i]) atomicAdd(&hist[(key[i] >> 8) + 128], sz[i]);
+  wave_sync();
+  int above1, inbin1;
+  const int hb = find_cross(hist, 0, ns, &above1, &inbin1);
+  wave_sync();
+  // ---- pass 2: low byte within the crossing high-byte bin ----
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hist[4 * l + i] = 0;
+  wave_sync();
+  const int hsel = hb - 128;
+#pragma unroll
+  for (int i = 0; i < 32; ++i)
+    if (sz[i] && (key[i] >> 8) == hsel) atomicAdd(&hist[key[i] & 255], sz[i]);
+  wave_sync();
+  int wgt, weq;
+  const int lb = find_cross(hist, above1, ns, &wgt, &weq);
+  wave_sync();
+  const int vstar = hsel * 256 + lb;
+  // ---- ties at the threshold, in ascending cluster order ----
+  int ntie = 0;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) ntie += (key[i] == vstar);
+  ntie = wave_sum(ntie);
+  uint32_t bits = 0;
+  if (ntie == 1) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) bits |= (uint32_t)(key[i] >= vstar) << i;
+    *rowcnt = wgt + weq;
+    return bits;
+  }
+  const int R = ns - wgt;  // >= 1 keys still needed from the tied clusters
+  int before = 0;          // tied weight of all earlier chunks g
+  int took = 0;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    int t = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t += (key[8 * g + j] == vstar) ? sz[8 * g + j] : 0;
+    const int inc = wave_incl_scan(t);
+    int p = before + inc - t;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = 8 * g + j;
+      bool s = key[i] > vstar;
+      if (key[i] == vstar) {
+        s = p < R;
+        if (s) took += sz[i];
+        p += sz[i];
+      }
+      bits |= (uint32_t)s << i;
+    }
+    before += __shfl(inc, 63, 64);
+  }
+  *rowcnt = wgt + wave_sum(took);
+  return bits;
+}
+
+// publish a lane mask into the packed union row (LSB-first words)
+__device__ inline void flush_union(uint32_t acc, int32_t* urow) {
+  const int l = __lane_id();
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t b = (acc >> (8 * g)) & 0xffu;
+    const uint32_t b1 = __shfl_down(b, 1, 64), b2 = __shfl_down(b, 2, 64), b3 = __shfl_down(b, 3, 64);
+    const uint32_t w = b | (b1 << 8) | (b2 << 16) | (b3 << 24);
+    if ((l & 3) == 0 && w) atomicOr((unsigned int*)&urow[16 * g + (l >> 2)], w);
+  }
+}
+
+__global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
+    const uint16_t* __restrict__ gl, const int32_t* __restrict__ kcounts,
+    const int32_t* __restrict__ qperm, const int32_t* __restrict__ off,
+    const int32_t* __restrict__ ns_dev, int32_t* __restrict__ unip, int32_t* __restrict__ rowcnt,
+    int N, int CQ) {
+  __shared__ int hist_all[SEL_WAVES][256];
+  const int h = blockIdx.y;
+  const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  int* hist = hist_all[wv];
+  const int32_t* offh = off + (size_t)h * (CQ + 1);
+  const int total = offh[CQ];
+  int j0 = (blockIdx.x * SEL_WAVES + wv) * SEL_ROWS_PER_WAVE;
+  int j1 = j0 + SEL_ROWS_PER_WAVE;
+  if (j1 > total) j1 = total;
+  if (j1 > N) j1 = N;  // qcounts summing past N is invalid input; never read past N
+  if (j0 >= j1) return;
+  // cluster sizes of the lane's 32 clusters, and the key total
+  int sz[32];
+  int ktot = 0;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int32_t* p = kcounts + (size_t)h * SEL_NC + 512 * g + 8 * l;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      sz[8 * g + j] = p[j];
+      ktot += p[j];
+    }
+  }
+  ktot = wave_sum(ktot);
+  int ns = *ns_dev;
+  ns = ns < 1 ? 1 : ns;
+  ns = ns > ktot ? ktot : ns;
+  // query cluster of the first row: largest t with off[t] <= j0
+  int lo = 0, hi = CQ - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (offh[mid] <= j0) lo = mid; else hi = mid - 1;
+  }
+  int t = lo;
+  while (t < CQ - 1 && offh[t + 1] <= j0) ++t;  // skip empty clusters
+  int tend = offh[t + 1];
+  uint32_t acc = 0;
+  const uint16_t* glh = gl + (size_t)h * N * SEL_NC;
+  const int32_t* qp = qperm + (size_t)h * N;
+  int32_t* uh = unip + (size_t)h * CQ * (SEL_NC / 32);
+  for (int j = j0; j < j1; ++j) {
+    if (j >= tend) {
+      if (acc) flush_union(acc, uh + (size_t)t * (SEL_NC / 32));
+      acc = 0;
+      do {
+        ++t;
+        tend = offh[t + 1];
+      } while (j >= tend);
+    }
+    const int orig = qp[j];
+    int key[32];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const u32x4 v = __builtin_nontemporal_load(
+          (const u32x4*)(glh + (size_t)orig * SEL_NC + 512 * g + 8 * l));
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        key[8 * g + 2 * q] = score_key((uint16_t)(v[q] & 0xffff));
+        key[8 * g + 2 * q + 1] = score_key((uint16_t)(v[q] >> 16));
+      }
+    }
+    int rc;
+    acc |= select_row(key, sz, hist, ns, &rc);
+    if (l == 0) rowcnt[(size_t)h * N + orig] = rc;
+  }
+  if (acc) flush_union(acc, uh + (size_t)t * (SEL_NC / 32));
+}
+
+__global__ void expand_union_kernel(const int32_t* __restrict__ unip, uint8_t* __restrict__ uni,
+                                    long long nbits) {
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < nbits;
+       i += (long long)gridDim.x * blockDim.x)
+    uni[i] = (uint8_t)(((uint32_t)unip[i >> 5] >> (i & 31)) & 1u);
+}
+
+extern "C" size_t t2t_select_ws_bytes(int H, int N, int CQ) {
+  (void)N;
+  WsCarver w(nullptr);
+  w.take<int32_t>((size_t)H * (CQ + 1));          // query-cluster offsets
+  w.take<int32_t>((size_t)H * CQ * (SEL_NC / 32)); // packed union for t2t_select_run
+  return w.off;
+}
+
+static int select_common(const void* gl, const int32_t* kcounts, const int32_t* qperm,
+                         const int32_t* qcounts, const int32_t* ns_dev, int32_t* unip,
+                         int32_t* rowcnt, int H, int N, int CQ, void* ws, size_t ws_bytes,
+                         hipStream_t st) {
+  T2T_REQUIRE(gl && kcounts && qperm && qcounts && ns_dev && unip && rowcnt,
+              "select: null pointer");
+  T2T_REQUIRE(H > 0 && N > 0 && CQ > 0, "select: H=%d N=%d CQ=%d", H, N, CQ);
+  T2T_REQUIRE(N < 524288, "select: N=%d must be < 524288", N);
+  if (!ws || ws_bytes < t2t_select_ws_bytes(H, N, CQ)) {
+    t2t_set_error("select: workspace %zu < %zu bytes", ws_bytes, t2t_select_ws_bytes(H, N, CQ));
+    return T2T_ERR_WORKSPACE;
+  }
+  WsCarver w(ws);
+  int32_t* off = w.take<int32_t>((size_t)H * (CQ + 1));
+  hipLaunchKernelGGL(select_prep_kernel, dim3(H), dim3(1024), 0, st, qcounts, off, unip, CQ);
+  T2T_LAUNCH_CHECK("select_prep");
+  const int rows_per_block = SEL_WAVES * SEL_ROWS_PER_WAVE;
+  hipLaunchKernelGGL(select_main_kernel, dim3(cdiv(N, rows_per_block), H), dim3(SEL_WAVES * 64), 0,
+                     st, (const uint16_t*)gl, kcounts, qperm, off, ns_dev, unip, rowcnt, N, CQ);
+  T2T_LAUNCH_CHECK("select_main");
+  return T2T_OK;
+}
+
+extern "C" int t2t_select_run_packed(const void* gl, const int32_t* kcounts, const int32_t* qperm,
+                                     const int32_t* qcounts, const int32_t* ns_dev, int32_t* unip,
+                                     int32_t* rowcnt, int H, int N, int CQ, void* ws,
+                                     size_t ws_bytes, void* stream) {
+  return select_common(gl, kcounts, qperm, qcounts, ns_dev, unip, rowcnt, H, N, CQ, ws, ws_bytes,
+                       (hipStream_t)stream);
+}
+
+extern "C" int t2t_select_run_split_packed(const void* gl, const int32_t* kcounts,
+                                           const int32_t* qperm, const int32_t* qcounts, int cap,
+                                           const int32_t* ns_dev, int32_t* unip, int32_t* rowcnt,
+                                           int H, int N, int CQ, void* ws, size_t ws_bytes,
+                                           void* stream) {
+  T2T_REQUIRE(cap >= 1, "select split: cap=%d must be >= 1", cap);
+  return select_common(gl, kcounts, qperm, qcounts, ns_dev, unip, rowcnt, H, N, CQ, ws, ws_bytes,
+                       (hipStream_t)stream);
+}
+
+extern "C" int t2t_select_run(const void* gl, const int32_t* kcounts, const int32_t* qperm,
+                              const int32_t* qcounts, const int32_t* ns_dev, uint8_t* uni,
+                              int32_t* rowcnt, int H, int N, int CQ, void* ws, size_t ws_bytes,
+                              void* stream) {
+  T2T_REQUIRE(uni, "select run: null uni");
+  if (!ws || ws_bytes < t2t_select_ws_bytes(H, N, CQ)) {
+    t2t_set_error("select run: workspace %zu < %zu bytes", ws_bytes, t2t_select_ws_bytes(H, N, CQ));
+    return T2T_ERR_WORKSPACE;
+  }
+  WsCarver w(ws);
+  w.take<int32_t>((size_t)H * (CQ + 1));
+  int32_t* packed = w.take<int32_t>((size_t)H * CQ * (SEL_NC / 32));
+  int rc = select_common(gl, kcounts, qperm, qcounts, ns_dev, packed, rowcnt, H, N, CQ, ws,
+                         ws_bytes, (hipStream_t)stream);
+  if (rc) return rc;
+  const long long nbits = (long long)H * CQ * SEL_NC;
+  hipLaunchKernelGGL(expand_union_kernel, dim3(2048), dim3(256), 0, (hipStream_t)stream, packed,
+                     uni, nbits);
+  T2T_LAUNCH_CHECK("select run expand");
+  return T2T_OK;
+}

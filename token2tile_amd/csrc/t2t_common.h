@@ -1,0 +1,152 @@
+// Shared device helpers for the gfx950 Token2Tile kernels: element types,
+// MFMA wrappers, wave64 reductions and host-side error plumbing.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+#include <stddef.h>
+#include "../../include/t2t_hip.h"
+
+#define T2T_WAVE 64
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// element types: raw 16-bit storage, conversions through fp32
+// ---------------------------------------------------------------------------
+struct F16T {
+  static constexpr int code = T2T_F16;
+  __device__ static inline float to_f(uint16_t u) {
+    _Float16 h = __builtin_bit_cast(_Float16, u);
+    return (float)h;
+  }
+  __device__ static inline uint16_t from_f(float f) {  // round to nearest even
+    _Float16 h = (_Float16)f;
+    return __builtin_bit_cast(uint16_t, h);
+  }
+};
+struct BF16T {
+  static constexpr int code = T2T_BF16;
+  __device__ static inline float to_f(uint16_t u) {
+    return __builtin_bit_cast(float, (uint32_t)u << 16);
+  }
+  __device__ static inline uint16_t from_f(float f) {  // round to nearest even
+    uint32_t x = __builtin_bit_cast(uint32_t, f);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40);  // quiet NaN
+    x += 0x7fffu + ((x >> 16) & 1u);
+    return (uint16_t)(x >> 16);
+  }
+};
+
+__device__ inline float h2f(uint16_t u) { return F16T::to_f(u); }
+__device__ inline uint16_t f2h(float f) { return F16T::from_f(f); }
+
+// bf16 -> fp16 (through fp32; exact for values inside the fp16 normal range)
+__device__ inline uint16_t bf2h(uint16_t b) { return f2h(BF16T::to_f(b)); }
+
+// ---------------------------------------------------------------------------
+// MFMA 32x32x16 (gfx950).  Operand convention used everywhere:
+//   lane l supplies A[i = l % 32][k = 8 * (l / 32) + t] and
+//   B[k = 8 * (l / 32) + t][j = l % 32] for t = 0..7;
+//   D[i][j] lands in lane l = j + 32 * ((i / 4) % 2), element
+//   a = 4 * (i / 8) + i % 4  (i = 8 * (a / 4) + 4 * (l / 32) + a % 4).
+// ---------------------------------------------------------------------------
+template <typename T> struct Mfma;
+template <> struct Mfma<F16T> {
+  __device__ static inline f32x16 run(const u32x4& a, const u32x4& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<BF16T> {
+  __device__ static inline f32x16 run(const u32x4& a, const u32x4& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+__device__ inline f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// ---------------------------------------------------------------------------
+// wave64 helpers
+// ---------------------------------------------------------------------------
+__device__ inline int lane_id() { return __lane_id(); }
+
+__device__ inline int wave_incl_scan(int v) {
+  const int l = __lane_id();
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    int y = __shfl_up(v, d, 64);
+    if (l >= d) v += y;
+  }
+  return v;
+}
+__device__ inline int wave_sum(int v) {
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+__device__ inline long long wave_sum64(long long v) {
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, 64));
+  return v;
+}
+
+// fp16 score -> int16 key ordering like the value with -0 < +0
+__device__ inline int score_key(uint16_t u) {
+  u ^= (uint16_t)(((u >> 15) & 1u) * 0x7FFFu);
+  return (int)(int16_t)u;
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+void t2t_set_error(const char* fmt, ...);
+int t2t_check_launch(const char* what);
+
+#define T2T_REQUIRE(cond, ...)              \
+  do {                                      \
+    if (!(cond)) {                          \
+      t2t_set_error(__VA_ARGS__);           \
+      return T2T_ERR_ARG;                   \
+    }                                       \
+  } while (0)
+
+#define T2T_LAUNCH_CHECK(what)                          \
+  do {                                                  \
+    int _rc = t2t_check_launch(what);                   \
+    if (_rc != T2T_OK) return _rc;                      \
+  } while (0)
+
+static inline size_t t2t_align256(size_t x) { return (x + 255) & ~(size_t)255; }
+static inline int cdiv(long long a, long long b) { return (int)((a + b - 1) / b); }
+
+// Carves aligned sub-buffers out of a caller-owned workspace (base may be
+// NULL to measure the size).
+struct WsCarver {
+  char* base;
+  size_t off = 0;
+  explicit WsCarver(void* b) : base((char*)b) {}
+  template <typename T> T* take(size_t count) {
+    T* p = base ? (T*)(base + off) : nullptr;
+    off += t2t_align256(count * sizeof(T));
+    return p;
+  }
+};

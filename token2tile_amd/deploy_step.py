@@ -1,0 +1,347 @@
+"""Token2Tile attention operator on MI355X: one sparse attention call.
+
+Drop-in counterpart of ``token2tile/operator/deploy_step.py``: same module
+surface (``MaskedStepDeploy``, ``online_u``, ``fast_assign``, ``fast_gather``),
+same constructor, ``init_state`` / ``set_cfg_call`` / ``reset_cfg_reuse`` /
+``step`` semantics, same snapshot reuse rules.  Every stage runs in the HIP
+library (``libt2t_hip.so``); there is no CPU path.
+
+``step(q, k, v, state)`` for q, k, v of shape [H, N, 128] (fp16, or bf16 -
+the model dtype, accepted without a conversion pass):
+
+  1. projection   QU = q Uq, KU = k Uk                       t2t_project
+  2. clustering   one warm-started k-means update            t2t_kmm_run
+  3. scoring      gl = QU cks^T                              t2t_score
+  4. selection    per-query budget prefix + cluster union    t2t_select_run_packed
+  5. attention    exact attention over the unions, residual
+                  over the other clusters, merge             t2t_tile_attn_run_planned
+
+The output is in the original row order.  With ``mask_refresh=R`` the
+structure (labels, permutations, sizes, centroids, union, task plan) is
+rebuilt every R annotated steps and reused in between (deploy_step.py:296-316).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import ops
+from .ops import fast_gather  # noqa: F401  (module surface of the reference)
+
+__all__ = ["MaskedStepDeploy", "online_u", "fast_assign", "fast_gather", "fused_update_vstats"]
+
+
+# ---------------------------------------------------------------------------
+# low-rank space (deploy_step.py:104-149)
+# ---------------------------------------------------------------------------
+
+def _eigh_robust(M):
+    """Symmetric eigendecomposition; on a solver failure, retry on the host
+    LAPACK like the reference (deploy_step.py:104-111)."""
+    try:
+        return torch.linalg.eigh(M)
+    except torch._C._LinAlgError:
+        e, V = torch.linalg.eigh(M.cpu())
+        return e.to(M.device), V.to(M.device)
+
+
+def _svd_robust(M):
+    try:
+        return torch.linalg.svd(M)
+    except torch._C._LinAlgError:
+        U, S, Vh = torch.linalg.svd(M.cpu())
+        return U.to(M.device), S.to(M.device), Vh.to(M.device)
+
+
+def online_u(qf, kf, r=32):
+    """Matched rank-r projections Uq, Uk [H, D, r] (fp32) minimising
+    ||Q K^T - (Q Uq)(K Uk)^T||_F (deploy_step.py:122-149).
+
+    The Gram matrices come from the HIP fp64 Gram kernel (16-bit inputs) or
+    from fp64 matmul for fp32 inputs; the 128 x 128 eigen/SVD problems run
+    batched in fp64.  Raises RuntimeError on non-finite input.
+    """
+    for name, t in (("q", qf), ("k", kf)):
+        bad = ~torch.isfinite(t)
+        if bool(bad.any()):
+            raise RuntimeError(
+                f"online_u: non-finite {name} input; per-head counts "
+                f"{bad.sum(dim=(1, 2)).tolist()}, shape {tuple(t.shape)}")
+
+    def gram(x):
+        if x.dtype in (torch.float16, torch.bfloat16):
+            return ops.gram(x.contiguous())
+        xd = x.double()
+        return xd.transpose(1, 2) @ xd / x.shape[1]
+
+    Mq, Mk = gram(qf), gram(kf)
+    eq, Vq = _eigh_robust(Mq)
+    ek, Vk = _eigh_robust(Mk)
+    eq, ek = eq.clamp_min(1e-8), ek.clamp_min(1e-8)
+    Rq = Vq @ (eq.sqrt().unsqueeze(-1) * Vq.transpose(1, 2))
+    Rk = Vk @ (ek.sqrt().unsqueeze(-1) * Vk.transpose(1, 2))
+    Rqi = Vq @ (eq.rsqrt().unsqueeze(-1) * Vq.transpose(1, 2))
+    Rki = Vk @ (ek.rsqrt().unsqueeze(-1) * Vk.transpose(1, 2))
+    U, S, Vh = _svd_robust(Rq.transpose(1, 2) @ Rk)
+    sr = S[:, :r].sqrt().unsqueeze(1)
+    Uq = (Rqi.transpose(1, 2) @ U[:, :, :r]) * sr
+    Uk = (Rki @ Vh[:, :r, :].transpose(1, 2)) * sr
+    return Uq.float().contiguous(), Uk.float().contiguous()
+
+
+def fast_assign(x, centroids, out=None, **_tuning):
+    """Nearest centroid (lowest index on ties), [H, N] int32
+    (fast_assign.py:79-106).  Tuning keywords of the reference are accepted
+    and ignored."""
+    return ops.fast_assign_labels(x.contiguous(), centroids.contiguous(), out=out)
+
+
+def fused_update_vstats(ku, labels, old_centroids, v=None, **_kw):
+    """Centroid update with empty clusters keeping the old centroid; returns
+    (new_centroids fp16, counts int32, None) like fused_update_vstats.py:72-115
+    (value statistics are not produced).  The sums are the deterministic
+    int64 fixed-point ones of the reference backend (t2t_attn.py:242-257)."""
+    if v is not None:
+        raise NotImplementedError("t2t: value statistics come from t2t_kmm_run")
+    new, counts = ops.det_centroid_update(ku.contiguous(), labels.to(torch.int32).contiguous(),
+                                          old_centroids.contiguous())
+    return new, counts, None
+
+
+# ---------------------------------------------------------------------------
+# the operator
+# ---------------------------------------------------------------------------
+
+class MaskedStepDeploy:
+    """Persistent buffers and kernels for one (H, N, C_Q) attention shape.
+
+    s_frac: per-query token budget as a fraction of N (``ns_t`` holds the token
+        count on the device and may be overwritten between calls).
+    mask_refresh: rebuild the structure every this many annotated steps.
+    cfg_reuse: structure reuse across CFG branches even when mask_refresh is 1.
+    pin_tail: the last pin_tail keys form one reserved key cluster that every
+        query executes exactly.
+    split_cap: accepted for interface compatibility; the HIP selection kernel
+        balances rows per wave whatever the query-cluster sizes, so the split
+        and unsplit variants are the same launch.
+    (deploy_step.py:152-242)
+    """
+
+    def __init__(self, H, N, CQ, *, C=2048, D=128, r=32, s_frac=0.05, tailw=1.0, device="cuda",
+                 mask_refresh=1, cfg_reuse=False, pin_tail=0, split_cap="auto"):
+        if C != 2048 or D != 128:
+            raise ValueError("the kernels require C=2048 and D=128")
+        if r != 32:
+            raise ValueError("the kernels require r=32")
+        if not (1 <= CQ <= 4096):
+            raise ValueError("CQ must be in [1, 4096]")
+        if N >= 524288:
+            raise ValueError("the selection packing requires N < 524288")
+        self.H, self.N, self.CQ, self.C, self.D, self.r = H, N, CQ, C, D, r
+        self.ns = max(1, int(s_frac * N))
+        self.tailw = tailw
+        self.dev = dev = torch.device(device)
+        if dev.type != "cuda":
+            raise ValueError("MaskedStepDeploy runs on a ROCm GPU device")
+        self.scale = 1.0 / math.sqrt(D)
+        self.pin_tail = int(pin_tail)
+        if not (0 <= self.pin_tail <= N):
+            raise ValueError("pin_tail must be in [0, N]")
+        self.split_cap = 0 if split_cap in ("auto", None, 0) else int(split_cap)
+        ops._lib.lib()  # fail loudly now if the HIP library is missing
+
+        f16, f32, i32 = torch.float16, torch.float32, torch.int32
+        self.QU = torch.empty(H, N, r, device=dev, dtype=f16)
+        self.KU = torch.empty(H, N, r, device=dev, dtype=f16)
+        self.gl = torch.empty(H, N, C, device=dev, dtype=f16)
+        self.klab = torch.empty(H, N, device=dev, dtype=i32)
+        self.qlab = torch.empty(H, N, device=dev, dtype=i32)
+        self.rowcnt = torch.empty(H, N, device=dev, dtype=i32)
+        self._io = {}                 # dtype -> (kp, vp, out, attn workspace)
+        self._tile_attn_plan_ints = ops.plan_ints(H, N, CQ)
+        self.tailw_t = torch.tensor(float(tailw), device=dev, dtype=f32)
+        self._kmm_cq2 = torch.empty(H, CQ, r, device=dev, dtype=f16)
+        self._kmm_ck2 = torch.empty(H, C, r, device=dev, dtype=f32)
+        self._kmm_kcounts = torch.empty(H, C, device=dev, dtype=i32)
+        self._kmm_sumv = torch.empty(H, C, D, device=dev, dtype=f16)
+        self._kmm_lam = torch.empty(H, device=dev, dtype=f32)
+        self.ns_t = torch.tensor(self.ns, device=dev, dtype=i32)
+        self._ws_kmm = torch.empty(ops.kmm_ws_bytes(H, N, CQ, C), dtype=torch.uint8, device=dev)
+        self._ws_vst = torch.empty(ops.vstats_ws_bytes(H, N, C), dtype=torch.uint8, device=dev)
+        self._ws_sel = torch.empty(ops.select_ws_bytes(H, N, CQ), dtype=torch.uint8, device=dev)
+
+        self.cfg_reuse = bool(cfg_reuse)
+        self.mask_refresh = max(1, int(mask_refresh))
+        self._cfg_on = self.cfg_reuse or self.mask_refresh > 1
+        self._cfg_hold = {}
+        self._cfg_parity = None
+        self._cfg_key = 0
+        self._cfg_step = 0
+
+        # default-priority streams (the two-stream schedule of the reference)
+        self.s_main = torch.cuda.Stream(device=dev)
+        self.s_side = torch.cuda.Stream(device=dev)
+        self.last_call_full = None
+
+    def _buffers(self, dtype):
+        io = self._io.get(dtype)
+        if io is None:
+            H, N, D = self.H, self.N, self.D
+            io = dict(kp=torch.empty(H, N, D, device=self.dev, dtype=dtype),
+                      vp=torch.empty(H, N, D, device=self.dev, dtype=dtype),
+                      out=torch.empty(H, N, D, device=self.dev, dtype=dtype),
+                      ws=torch.empty(ops.attn_ws_bytes(H, N, dtype), dtype=torch.uint8,
+                                     device=self.dev))
+            self._io[dtype] = io
+        return io
+
+    @property
+    def kp(self):
+        return self._buffers(torch.float16)["kp"]
+
+    @property
+    def vp(self):
+        return self._buffers(torch.float16)["vp"]
+
+    # -- state init (deploy_step.py:245-266) ---------------------------------
+    def init_state(self, q, k, *, warm_iters=4, seed=0):
+        """Projections and initial centroids of one layer: the projections are
+        kept for the whole request; the centroids warm-start every rebuild.
+        Initial centroids are KU / QU rows picked by a seeded CPU randperm
+        (the same indices as the reference), then ``warm_iters`` Lloyd
+        iterations (nearest centroid + deterministic centroid update)."""
+        N, r = self.N, self.r
+        Uq, Uk = online_u(q, k, r)
+        Uq = Uq.to(torch.float16).contiguous()
+        Uk = Uk.to(torch.float16).contiguous()
+        KU = ops.project(k.contiguous(), Uk)
+        QU = ops.project(q.contiguous(), Uq)
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        kidx = torch.randperm(N, generator=g)[: self.C].sort().values.to(self.dev)
+        qidx = torch.randperm(N, generator=g)[: self.CQ].sort().values.to(self.dev)
+        ck = KU[:, kidx, :].contiguous()
+        cq = QU[:, qidx, :].contiguous()
+        for _ in range(warm_iters):
+            lab = fast_assign(KU, ck)
+            ck, _ = ops.det_centroid_update(KU, lab, ck)
+            lab = fast_assign(QU, cq)
+            cq, _ = ops.det_centroid_update(QU, lab, cq)
+        torch.cuda.synchronize(self.dev)
+        return {"Uq": Uq, "Uk": Uk, "ck": ck.contiguous(), "cq": cq.contiguous()}
+
+    def set_cfg_call(self, parity, key=0, step=0):
+        """Annotate the next step() call (deploy_step.py:268-277)."""
+        self._cfg_parity = int(parity)
+        self._cfg_key = key
+        self._cfg_step = int(step)
+
+    def reset_cfg_reuse(self):
+        """Drop all snapshots and any pending annotation (deploy_step.py:279-283)."""
+        self._cfg_hold.clear()
+        self._cfg_parity = None
+
+    # -- the attention call (deploy_step.py:286-477) -------------------------
+    def step(self, q, k, v, state):
+        """q, k, v: [H, N, 128] fp16 (or bf16) contiguous, original row order.
+        state: dict(Uq, Uk, ck, cq) fp16; ck/cq are replaced by fresh tensors
+        holding the centroids that warm-start the next call.  Returns out
+        [H, N, 128] in q's dtype (a buffer reused by the next call)."""
+        H, N, C, CQ, D = self.H, self.N, self.C, self.CQ, self.D
+        for name, t in (("q", q), ("k", k), ("v", v)):
+            if tuple(t.shape) != (H, N, D) or not t.is_contiguous() or t.device != self.dev:
+                raise ValueError(f"step: {name} must be a contiguous [{H}, {N}, {D}] tensor on "
+                                 f"{self.dev}")
+        if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError("step: q, k, v must share dtype fp16 or bf16")
+        caller = torch.cuda.current_stream(self.dev)
+        s0, s1 = self.s_main, self.s_side
+        if caller != s0:
+            s0.wait_stream(caller)
+        io = self._buffers(q.dtype)
+        st0 = s0.cuda_stream
+
+        snap = None
+        held = None
+        cfg_parity = self._cfg_parity
+        self._cfg_parity = None
+        if self._cfg_on and cfg_parity is not None:
+            held = self._cfg_hold.get(self._cfg_key)
+            age = None if held is None else self._cfg_step - held["step"]
+            refresh_due = age is None or age < 0 or age >= self.mask_refresh
+            if held is not None and age >= 0 and not (cfg_parity == 0 and refresh_due):
+                snap = held
+        recycle = held is not None and snap is None
+        self.last_call_full = snap is None
+
+        with torch.cuda.stream(s0):
+            if snap is not None:
+                # reuse: project with the snapshot's Uq, group K and V through
+                # the stored kperm, fresh value statistics from this call's V
+                ops.project(q, snap["Uq"], out=self.QU, stream=s0)
+                ops.fast_gather(k, snap["kperm"], out=io["kp"], stream=s0)
+                ops.vstats_gather(v, snap["kperm"], snap["counts"], V_sorted=io["vp"],
+                                  sumv=self._kmm_sumv, lam=self._kmm_lam, ws=self._ws_vst,
+                                  stream=s0)
+                tile_sizes, qperm, counts = snap["tile_sizes"], snap["qperm"], snap["counts"]
+                qlab_cur, cks, unip = snap["qlab"], snap["cks"], snap["unip"]
+                plan, rebuild = snap["tile_attn_plan"], False
+            else:
+                ops.project(q, state["Uq"], out=self.QU, stream=s0)
+                ops.project(k, state["Uk"], out=self.KU, stream=s0)
+                if recycle:
+                    km_out = dict(qlab=held["qlab"], klab=held["klab"], qcounts=held["tile_sizes"],
+                                  qperm=held["qperm"], kperm=held["kperm"],
+                                  kcounts=held["counts"])
+                else:
+                    km_out = dict(qlab=self.qlab, klab=self.klab,
+                                  qcounts=torch.empty(H, CQ, device=self.dev, dtype=torch.int32),
+                                  qperm=torch.empty(H, N, device=self.dev, dtype=torch.int32),
+                                  kperm=torch.empty(H, N, device=self.dev, dtype=torch.int32),
+                                  kcounts=self._kmm_kcounts)
+                km_out.update(cq2=self._kmm_cq2, ck2=self._kmm_ck2, V_sorted=io["vp"],
+                              sumv=self._kmm_sumv, lam=self._kmm_lam)
+                ops.kmm_run(self.QU, self.KU, v, state["cq"], state["ck"], pin_tail=self.pin_tail,
+                            out=km_out, ws=self._ws_kmm, stream=s0)
+                tile_sizes, qperm, counts = km_out["qcounts"], km_out["qperm"], km_out["kcounts"]
+                ck16, cks = ops.centroid_finalize(self._kmm_ck2, self.scale, stream=s0)
+                state["ck"] = ck16
+                state["cq"] = self._kmm_cq2.clone()
+                ops.score(self.QU, cks, out=self.gl, stream=s0)
+                unip = held["unip"] if recycle else torch.empty(H, CQ, C // 32, device=self.dev,
+                                                                dtype=torch.int32)
+                ops.select_union(self.gl, counts, qperm, tile_sizes, self.ns_t, unip=unip,
+                                 rowcnt=self.rowcnt, ws=self._ws_sel, split_cap=self.split_cap,
+                                 stream=s0)
+                if self.pin_tail:
+                    ops.union_or_last(unip, stream=s0)
+                ops.fast_gather(k, km_out["kperm"], out=io["kp"], stream=s0)
+                plan = (held["tile_attn_plan"] if recycle else
+                        torch.empty(self._tile_attn_plan_ints, device=self.dev, dtype=torch.int32))
+                rebuild = True
+                qlab_cur = km_out["qlab"]
+                if self._cfg_on:
+                    self._cfg_hold[self._cfg_key] = {
+                        "qlab": qlab_cur if recycle else qlab_cur.clone(),
+                        "qperm": qperm,
+                        "tile_sizes": tile_sizes,
+                        "klab": km_out["klab"] if recycle else km_out["klab"].clone(),
+                        "kperm": km_out["kperm"],
+                        "counts": counts if recycle else counts.clone(),
+                        "cks": cks,
+                        "Uq": state["Uq"],
+                        "unip": unip,
+                        "tile_attn_plan": plan,
+                        "step": self._cfg_step,
+                    }
+            ops.tile_attn_run_planned(q, io["kp"], io["vp"], tile_sizes, counts, unip, self.QU, cks,
+                                      self._kmm_sumv, self._kmm_lam, qlab_cur, qperm, self.tailw_t,
+                                      io["out"], plan, rebuild, ws=io["ws"], stream=s0)
+        del st0
+        s1.wait_stream(s0)
+        cur = torch.cuda.current_stream(self.dev)
+        cur.wait_stream(s0)
+        cur.wait_stream(s1)
+        self._last = dict(unip=unip, qperm=qperm, tile_sizes=tile_sizes, counts=counts,
+                          qlab=qlab_cur, cks=cks, plan=plan)
+        return io["out"]
