@@ -1,0 +1,221 @@
+"""Benchmark of one Token2Tile attention call on one MI355X.
+
+Metric: T2T attention ms/call + TFLOPS at 75.6k tokens,
+40 heads, d=128; speedup vs dense.  Workload: the Wan2.1-14B 720p shape
+(H=40, N=75600, 1.5% budget, 512 query clusters) on seeded synthetic
+Gaussian-mixture inputs in bf16, resident in HBM.
+
+One step = one MaskedStepDeploy.step call under the reuse schedule
+mask_refresh=4 (a structure-rebuilding call every 4th step, reuse calls in
+between), so ms/step is the R=4-weighted mean.  Full and reuse calls are
+also timed separately, per stage, with HIP events on the operator's stream.
+
+Also measured: dense bf16 attention on the same GPU (this library's tile
+kernel with an all-ones union, and torch SDPA), the roofline fraction of
+the tile-attention kernel, and the CPU oracle on the CPU plumbing config.
+
+Prints one JSON line.  Usage: python bench.py [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=12)
+    p.add_argument("--warmup", type=int, default=4)
+    p.add_argument("--config", default="wan720p")
+    p.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-dense", action="store_true")
+    p.add_argument("--sdpa", action="store_true", help="also time torch SDPA (slow at 720p)")
+    return p.parse_args()
+
+
+def cpu_baseline():
+    """The CPU oracle (numpy restatement of the reference semantics) timed
+    on one full call of the CPU plumbing config."""
+    import numpy as np
+    from oracle import t2t_oracle as O
+    from token2tile_amd.synth import CONFIGS, budget, generate_np
+    H, N, grid, frac, CQ = CONFIGS["cpu_plumbing"]
+    q, k, v = generate_np(H, N, grid=grid, seed=0)
+    Uq, Uk = O.online_u(q, k, 32)
+    Uq, Uk = Uq.astype(np.float16), Uk.astype(np.float16)
+    QU, KU = O.project(q, Uq), O.project(k, Uk)
+    rng = np.random.default_rng(0)
+    st = dict(Uq=Uq, Uk=Uk, ck=KU[:, np.sort(rng.choice(N, 2048, replace=False))],
+              cq=QU[:, np.sort(rng.choice(N, CQ, replace=False))])
+    t0 = time.perf_counter()
+    O.full_call(q, k, v, st, budget(N, frac), CQ)
+    dt = time.perf_counter() - t0
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(dt * 1e3, 1), "unit": "ms/call", "cores": threads, "kind": "port",
+            "sample": f"one structure-rebuilding call of the numpy oracle on the CPU plumbing "
+                      f"config (H={H}, N={N}, CQ={CQ}, ns={budget(N, frac)}, fp32/fp64)"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (heads shard "
+                                   "across GPUs outside the operator)"}))
+        sys.exit(2)
+    import torch
+    from token2tile_amd import ops
+    from token2tile_amd.deploy_step import MaskedStepDeploy
+    from token2tile_amd.synth import CONFIGS, budget, generate
+
+    H, N, grid, frac, CQ = CONFIGS[args.config]
+    dt = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+    dev = torch.device("cuda", 0)
+    print(f"[bench] config={args.config} H={H} N={N} CQ={CQ} ns={budget(N, frac)} dtype={args.dtype}",
+          file=sys.stderr, flush=True)
+    q, k, v = generate(H, N, grid=grid, seed=0, device=dev, dtype=dt)
+    deploy = MaskedStepDeploy(H, N, CQ, s_frac=frac, mask_refresh=4, device=dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    state = deploy.init_state(q, k, seed=0)
+    torch.cuda.synchronize()
+    init_ms = (time.perf_counter() - t0) * 1e3
+    print(f"[bench] init_state {init_ms:.1f} ms", file=sys.stderr, flush=True)
+
+    step_no = [0]
+
+    def one_step(record=None):
+        deploy.set_cfg_call(0, key=0, step=step_no[0])
+        step_no[0] += 1
+        deploy.stage_events = record
+        out = deploy.step(q, k, v, state)
+        deploy.stage_events = None
+        return out
+
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    # timed region: exactly K steps
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one_step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    print(f"[bench] {args.steps} steps: {wall_ms:.3f} ms/step", file=sys.stderr, flush=True)
+
+    # per-stage event timing of one full and three reuse calls
+    stages = {"full": {}, "reuse": {}}
+    call_ms = {"full": [], "reuse": []}
+    for _ in range(8):
+        ev = []
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        one_step(ev)
+        b.record()
+        torch.cuda.synchronize()
+        kind = "full" if deploy.last_call_full else "reuse"
+        call_ms[kind].append(a.elapsed_time(b))
+        for name, e0, e1 in ev:
+            stages[kind].setdefault(name, []).append(e0.elapsed_time(e1))
+    stage_ms = {kd: {n: round(sum(x) / len(x), 4) for n, x in d.items()} for kd, d in stages.items()}
+    full_ms = sum(call_ms["full"]) / max(1, len(call_ms["full"]))
+    reuse_ms = sum(call_ms["reuse"]) / max(1, len(call_ms["reuse"]))
+    print(f"[bench] full {full_ms:.3f} ms, reuse {reuse_ms:.3f} ms, stages {stage_ms}",
+          file=sys.stderr, flush=True)
+
+    # executed attention work: 4 * D * sum_t rows_t * kv_len_t
+    snap = deploy._cfg_hold[0]
+    pv = ops.plan_views(snap["tile_attn_plan"], H, N, CQ)
+    rows_kv = (pv["kvlen"].long() * snap["tile_sizes"].long()).sum().item()
+    attn_flops = 4.0 * 128 * rows_kv
+    tail_flops = 2.0 * H * N * 2048 * (32 + 128)
+    dense_flops = 4.0 * H * N * N * 128
+    attn_ms = stage_ms["reuse"].get("attention", stage_ms["full"]["attention"])
+    attn_tflops = attn_flops / (attn_ms * 1e-3) / 1e12
+    value = wall_ms
+
+    result_dense = {}
+    if not args.no_dense:
+        # dense baseline 1: this library's tile kernel over an all-ones union
+        ones = torch.full((H, CQ, 64), -1, dtype=torch.int32, device=dev)
+        plan = ops.tile_plan(snap["tile_sizes"], snap["counts"], ones, N)
+        io = deploy._buffers(dt)
+        ops.tile_attn_exact(q, io["kp"], io["vp"], snap["counts"], ones, snap["qperm"], plan,
+                            attn_out=io["attn_out"], lse=io["lse"])
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        reps = 2
+        a.record()
+        for _ in range(reps):
+            ops.tile_attn_exact(q, io["kp"], io["vp"], snap["counts"], ones, snap["qperm"], plan,
+                                attn_out=io["attn_out"], lse=io["lse"])
+        b.record()
+        torch.cuda.synchronize()
+        dense_ms = a.elapsed_time(b) / reps
+        result_dense["dense_tile_kernel_ms"] = round(dense_ms, 3)
+        result_dense["dense_tile_kernel_tflops"] = round(dense_flops / (dense_ms * 1e-3) / 1e12, 1)
+        if args.sdpa:
+            qq, kk, vv = (x.unsqueeze(0) for x in (q, k, v))
+            torch.nn.functional.scaled_dot_product_attention(qq, kk, vv)
+            torch.cuda.synchronize()
+            a.record()
+            torch.nn.functional.scaled_dot_product_attention(qq, kk, vv)
+            b.record()
+            torch.cuda.synchronize()
+            result_dense["dense_sdpa_ms"] = round(a.elapsed_time(b), 3)
+        best_dense = min(v_ for k_, v_ in result_dense.items() if k_.endswith("_ms"))
+        result_dense["speedup_vs_dense"] = round(best_dense / value, 3)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline (oracle, cpu plumbing config)...", file=sys.stderr, flush=True)
+        cpu = cpu_baseline()
+
+    out = {
+        "metric": "T2T attention ms/call + TFLOPS @75.6k tok, 40 heads, d128; speedup vs dense",
+        "value": round(value, 4),
+        "unit": "ms/call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic (seeded Gaussian-mixture Q/K with 3-D positional drift, N(0,1) V)",
+        "config": {"workload": f"{args.config}: one T2T attention call, mask_refresh=4 schedule",
+                   "heads": H, "tokens": N, "head_dim": 128, "key_clusters": 2048,
+                   "query_clusters": CQ, "budget_tokens": budget(N, frac), "rank": 32},
+        "full_call_ms": round(full_ms, 3),
+        "reuse_call_ms": round(reuse_ms, 3),
+        "stage_ms": stage_ms,
+        "init_state_ms": round(init_ms, 1),
+        "effective_tflops": round(dense_flops / (value * 1e-3) / 1e12, 1),
+        "executed_tflops": round((attn_flops + tail_flops) / (value * 1e-3) / 1e12, 1),
+        "mean_kv_len": round(rows_kv / (H * N), 1),
+        **result_dense,
+        "roofline": {"bound": "mfma", "kernel": "attn_kernel (tile attention)",
+                     "achieved": round(attn_tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(attn_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

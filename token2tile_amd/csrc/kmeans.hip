@@ -296,10 +296,10 @@ __global__ __launch_bounds__(256) void fixed_mean_kernel(const uint16_t* __restr
     if (n == 0) {
       v = old[o];
     } else if (MODE == 0) {
-      v = f2h((float)S / (32768.0f * (float)n));
+      v = f2h(opaque((float)S / (32768.0f * (float)n)));
     } else {
       const double m = ((double)S / 1048576.0) / (double)n;
-      v = f2h((float)m);
+      v = f2h(opaque((float)m));
     }
     out[o] = v;
   }
@@ -376,7 +376,7 @@ __global__ __launch_bounds__(1024) void vstats_kernel(const float* __restrict__ 
   const float inv = 1.0f / lm;
   if (tid == 0) lam[h] = lm;
   uint16_t* sh = sumv + (size_t)h * CE;
-  for (size_t i = tid; i < CE; i += 1024) sh[i] = f2h(vh[i] * inv);
+  for (size_t i = tid; i < CE; i += 1024) sh[i] = f2h(opaque(vh[i] * inv));
 }
 
 // ---------------------------------------------------------------------------

@@ -70,7 +70,7 @@ __global__ __launch_bounds__(256) void centroid_finalize_kernel(const float* __r
        i += (long long)gridDim.x * blockDim.x) {
     const float v = ck2[i];
     if (ck16) ck16[i] = f2h(v);
-    if (cks) cks[i] = f2h(__fmul_rn(v, scale));
+    if (cks) cks[i] = f2h(opaque(v * scale));
   }
 }
 

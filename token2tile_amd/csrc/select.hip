@@ -155,7 +155,8 @@ __device__ inline uint32_t select_row(const int (&key)[32], const int (&sz)[32],
   return bits;
 }
 
-// publish a lane mask into the packed union row (LSB-first words)
+// publish the lanes' masks into the packed union row (LSB-first words);
+// must be called by the whole wave (it shuffles across lanes)
 __device__ inline void flush_union(uint32_t acc, int32_t* urow) {
   const int l = __lane_id();
 #pragma unroll
@@ -213,8 +214,8 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
   const int32_t* qp = qperm + (size_t)h * N;
   int32_t* uh = unip + (size_t)h * CQ * (SEL_NC / 32);
   for (int j = j0; j < j1; ++j) {
-    if (j >= tend) {
-      if (acc) flush_union(acc, uh + (size_t)t * (SEL_NC / 32));
+    if (j >= tend) {  // wave-uniform: every lane takes part in the shuffles
+      flush_union(acc, uh + (size_t)t * (SEL_NC / 32));
       acc = 0;
       do {
         ++t;
@@ -237,7 +238,7 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
     acc |= select_row(key, sz, hist, ns, &rc);
     if (l == 0) rowcnt[(size_t)h * N + orig] = rc;
   }
-  if (acc) flush_union(acc, uh + (size_t)t * (SEL_NC / 32));
+  flush_union(acc, uh + (size_t)t * (SEL_NC / 32));
 }
 
 __global__ void expand_union_kernel(const int32_t* __restrict__ unip, uint8_t* __restrict__ uni,

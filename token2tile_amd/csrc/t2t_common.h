@@ -46,6 +46,14 @@ struct BF16T {
 };
 
 __device__ inline float h2f(uint16_t u) { return F16T::to_f(u); }
+
+// Materialise an fp32 value: keeps the compiler from fusing the operation
+// that produced it with a following fp16 conversion into one mixed-precision
+// instruction (which rounds once instead of fp32-then-fp16).
+__device__ inline float opaque(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 __device__ inline uint16_t f2h(float f) { return F16T::from_f(f); }
 
 // bf16 -> fp16 (through fp32; exact for values inside the fp16 normal range)

@@ -13,8 +13,10 @@ the model dtype, accepted without a conversion pass):
   2. clustering   one warm-started k-means update            t2t_kmm_run
   3. scoring      gl = QU cks^T                              t2t_score
   4. selection    per-query budget prefix + cluster union    t2t_select_run_packed
-  5. attention    exact attention over the unions, residual
-                  over the other clusters, merge             t2t_tile_attn_run_planned
+  5. attention    task plan, exact attention over the unions,
+                  residual over the other clusters, merge    t2t_tile_plan,
+                                                             t2t_tile_attn_exact,
+                                                             t2t_tail_merge
 
 The output is in the original row order.  With ``mask_refresh=R`` the
 structure (labels, permutations, sizes, centroids, union, task plan) is
@@ -183,6 +185,25 @@ class MaskedStepDeploy:
         self.s_main = torch.cuda.Stream(device=dev)
         self.s_side = torch.cuda.Stream(device=dev)
         self.last_call_full = None
+        # optional list: (stage name, start event, end event) per launch group
+        # recorded on s_main, for the benchmark's per-kernel timing
+        self.stage_events = None
+
+    def _stage(self, name):
+        deploy = self
+
+        class _Ctx:
+            def __enter__(self_):
+                if deploy.stage_events is not None:
+                    self_.a = torch.cuda.Event(enable_timing=True)
+                    self_.a.record(deploy.s_main)
+
+            def __exit__(self_, *exc):
+                if deploy.stage_events is not None:
+                    b = torch.cuda.Event(enable_timing=True)
+                    b.record(deploy.s_main)
+                    deploy.stage_events.append((name, self_.a, b))
+        return _Ctx()
 
     def _buffers(self, dtype):
         io = self._io.get(dtype)
@@ -191,8 +212,8 @@ class MaskedStepDeploy:
             io = dict(kp=torch.empty(H, N, D, device=self.dev, dtype=dtype),
                       vp=torch.empty(H, N, D, device=self.dev, dtype=dtype),
                       out=torch.empty(H, N, D, device=self.dev, dtype=dtype),
-                      ws=torch.empty(ops.attn_ws_bytes(H, N, dtype), dtype=torch.uint8,
-                                     device=self.dev))
+                      attn_out=torch.empty(H, N, D, device=self.dev, dtype=dtype),
+                      lse=torch.empty(H, N, device=self.dev, dtype=torch.float32))
             self._io[dtype] = io
         return io
 
@@ -259,7 +280,6 @@ class MaskedStepDeploy:
         if caller != s0:
             s0.wait_stream(caller)
         io = self._buffers(q.dtype)
-        st0 = s0.cuda_stream
 
         snap = None
         held = None
@@ -278,17 +298,21 @@ class MaskedStepDeploy:
             if snap is not None:
                 # reuse: project with the snapshot's Uq, group K and V through
                 # the stored kperm, fresh value statistics from this call's V
-                ops.project(q, snap["Uq"], out=self.QU, stream=s0)
-                ops.fast_gather(k, snap["kperm"], out=io["kp"], stream=s0)
-                ops.vstats_gather(v, snap["kperm"], snap["counts"], V_sorted=io["vp"],
-                                  sumv=self._kmm_sumv, lam=self._kmm_lam, ws=self._ws_vst,
-                                  stream=s0)
+                with self._stage("project"):
+                    ops.project(q, snap["Uq"], out=self.QU, stream=s0)
+                with self._stage("gather_k"):
+                    ops.fast_gather(k, snap["kperm"], out=io["kp"], stream=s0)
+                with self._stage("vstats"):
+                    ops.vstats_gather(v, snap["kperm"], snap["counts"], V_sorted=io["vp"],
+                                      sumv=self._kmm_sumv, lam=self._kmm_lam, ws=self._ws_vst,
+                                      stream=s0)
                 tile_sizes, qperm, counts = snap["tile_sizes"], snap["qperm"], snap["counts"]
                 qlab_cur, cks, unip = snap["qlab"], snap["cks"], snap["unip"]
                 plan, rebuild = snap["tile_attn_plan"], False
             else:
-                ops.project(q, state["Uq"], out=self.QU, stream=s0)
-                ops.project(k, state["Uk"], out=self.KU, stream=s0)
+                with self._stage("project"):
+                    ops.project(q, state["Uq"], out=self.QU, stream=s0)
+                    ops.project(k, state["Uk"], out=self.KU, stream=s0)
                 if recycle:
                     km_out = dict(qlab=held["qlab"], klab=held["klab"], qcounts=held["tile_sizes"],
                                   qperm=held["qperm"], kperm=held["kperm"],
@@ -301,21 +325,25 @@ class MaskedStepDeploy:
                                   kcounts=self._kmm_kcounts)
                 km_out.update(cq2=self._kmm_cq2, ck2=self._kmm_ck2, V_sorted=io["vp"],
                               sumv=self._kmm_sumv, lam=self._kmm_lam)
-                ops.kmm_run(self.QU, self.KU, v, state["cq"], state["ck"], pin_tail=self.pin_tail,
-                            out=km_out, ws=self._ws_kmm, stream=s0)
+                with self._stage("kmeans"):
+                    ops.kmm_run(self.QU, self.KU, v, state["cq"], state["ck"],
+                                pin_tail=self.pin_tail, out=km_out, ws=self._ws_kmm, stream=s0)
                 tile_sizes, qperm, counts = km_out["qcounts"], km_out["qperm"], km_out["kcounts"]
-                ck16, cks = ops.centroid_finalize(self._kmm_ck2, self.scale, stream=s0)
-                state["ck"] = ck16
-                state["cq"] = self._kmm_cq2.clone()
-                ops.score(self.QU, cks, out=self.gl, stream=s0)
+                with self._stage("score"):
+                    ck16, cks = ops.centroid_finalize(self._kmm_ck2, self.scale, stream=s0)
+                    state["ck"] = ck16
+                    state["cq"] = self._kmm_cq2.clone()
+                    ops.score(self.QU, cks, out=self.gl, stream=s0)
                 unip = held["unip"] if recycle else torch.empty(H, CQ, C // 32, device=self.dev,
                                                                 dtype=torch.int32)
-                ops.select_union(self.gl, counts, qperm, tile_sizes, self.ns_t, unip=unip,
-                                 rowcnt=self.rowcnt, ws=self._ws_sel, split_cap=self.split_cap,
-                                 stream=s0)
-                if self.pin_tail:
-                    ops.union_or_last(unip, stream=s0)
-                ops.fast_gather(k, km_out["kperm"], out=io["kp"], stream=s0)
+                with self._stage("select"):
+                    ops.select_union(self.gl, counts, qperm, tile_sizes, self.ns_t, unip=unip,
+                                     rowcnt=self.rowcnt, ws=self._ws_sel,
+                                     split_cap=self.split_cap, stream=s0)
+                    if self.pin_tail:
+                        ops.union_or_last(unip, stream=s0)
+                with self._stage("gather_k"):
+                    ops.fast_gather(k, km_out["kperm"], out=io["kp"], stream=s0)
                 plan = (held["tile_attn_plan"] if recycle else
                         torch.empty(self._tile_attn_plan_ints, device=self.dev, dtype=torch.int32))
                 rebuild = True
@@ -334,10 +362,18 @@ class MaskedStepDeploy:
                         "tile_attn_plan": plan,
                         "step": self._cfg_step,
                     }
-            ops.tile_attn_run_planned(q, io["kp"], io["vp"], tile_sizes, counts, unip, self.QU, cks,
-                                      self._kmm_sumv, self._kmm_lam, qlab_cur, qperm, self.tailw_t,
-                                      io["out"], plan, rebuild, ws=io["ws"], stream=s0)
-        del st0
+            # step 5: plan (structure rebuilds only), exact attention over the
+            # unions, residual over the other clusters and the merge
+            if rebuild:
+                with self._stage("plan"):
+                    ops.tile_plan(tile_sizes, counts, unip, N, plan=plan, stream=s0)
+            with self._stage("attention"):
+                ops.tile_attn_exact(q, io["kp"], io["vp"], counts, unip, qperm, plan,
+                                    attn_out=io["attn_out"], lse=io["lse"], stream=s0)
+            with self._stage("tail"):
+                ops.tail_merge(io["attn_out"], io["lse"], self.QU, cks, self._kmm_sumv,
+                               counts, unip, qlab_cur, qperm, self._kmm_lam, self.tailw_t,
+                               out=io["out"], stream=s0)
         s1.wait_stream(s0)
         cur = torch.cuda.current_stream(self.dev)
         cur.wait_stream(s0)
