@@ -264,7 +264,7 @@ def test_plan(dev):
         tasks = pv["tasks"][h, :nt]
         covered = np.zeros(N, dtype=int)
         for t, s, rows, _ in tasks:
-            assert 1 <= rows <= 128 and qoff[h, t] <= s and s + rows <= qoff[h, t] + qcounts[h, t]
+            assert 1 <= rows <= 256 and qoff[h, t] <= s and s + rows <= qoff[h, t] + qcounts[h, t]
             covered[s:s + rows] += 1
         assert np.all(covered == 1)
         work = tasks[:, 2].astype(np.int64) * kvlen[h, tasks[:, 0]]

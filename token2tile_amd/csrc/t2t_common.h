@@ -37,11 +37,8 @@ struct BF16T {
   __device__ static inline float to_f(uint16_t u) {
     return __builtin_bit_cast(float, (uint32_t)u << 16);
   }
-  __device__ static inline uint16_t from_f(float f) {  // round to nearest even
-    uint32_t x = __builtin_bit_cast(uint32_t, f);
-    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40);  // quiet NaN
-    x += 0x7fffu + ((x >> 16) & 1u);
-    return (uint16_t)(x >> 16);
+  __device__ static inline uint16_t from_f(float f) {  // round to nearest even (v_cvt_pk_bf16_f32)
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
   }
 };
 

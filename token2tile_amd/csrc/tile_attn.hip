@@ -1,12 +1,15 @@
 // S5/S6: task planning, exact attention over each query cluster's union of
 // key clusters, and the centroid residual + merge (gfx950, MFMA 32x32x16).
 //
-// Exact attention (one work-group per task of <= 128 sorted queries of one
-// query cluster, 4 waves x 32 queries):
+// Exact attention (one work-group per task of <= 256 sorted queries of one
+// query cluster, 8 waves x 32 queries):
 //   * the union is turned into runs of cluster-ordered key rows in LDS;
 //   * 64-key tiles of K (row major) and V (transposed, key-contiguous) are
-//     gathered from kp/vp into LDS, the next tile's global loads in flight
-//     while the current one is consumed;
+//     gathered from kp/vp into a double-buffered LDS ring: tile t is consumed
+//     while tile t+1 is written from registers and tile t+2 is in flight, one
+//     barrier per tile;
+//   * the running max advances with a margin, so O is rescaled only when a
+//     tile raises the max by more than the margin;
 //   * S^T = K Q^T and O^T = V^T P^T on MFMA, so every lane owns one query:
 //     the online-softmax max/sum need one cross-half exchange, and the
 //     per-query rescale of O touches only the lane's own registers.
@@ -17,7 +20,8 @@
 
 #define TA_D 128
 #define TA_CK 2048
-#define TA_QT 128   // queries per task (4 waves x 32)
+#define TA_QT 256   // queries per task (8 waves x 32)
+#define TA_WAVES 8
 #define TA_KT 64    // keys per tile
 #define TA_KP 136   // sK pitch (halves)
 #define TA_VP 68    // sVt pitch (halves)
@@ -208,19 +212,21 @@ __device__ inline int xcd_remap(int bid, int total) {
   return (bid % 8) * per + bid / 8;
 }
 
+#define TA_MARGIN 3.0f  // log2 units of headroom when the running max advances
+
 template <typename T>
-__global__ __launch_bounds__(256) void attn_kernel(
+__global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kp,
     const uint16_t* __restrict__ vp, const uint32_t* __restrict__ unip,
     const int32_t* __restrict__ qperm, const int32_t* __restrict__ kcounts,
     const int32_t* __restrict__ k_off, const int32_t* __restrict__ ntask,
     const int32_t* __restrict__ tasks, uint16_t* __restrict__ out, float* __restrict__ lse,
     int H, int N, int CQ, int maxT) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[TA_KT * TA_KP];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[TA_D * TA_VP];
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][TA_KT * TA_KP];
+  __shared__ __attribute__((aligned(16))) uint16_t sVt[2][TA_D * TA_VP];
   __shared__ int runStart[TA_CK];
   __shared__ int runCum[TA_CK + 1];
-  __shared__ int wsc[4], wsr[4];
+  __shared__ int wsc[TA_WAVES], wsr[TA_WAVES];
   const int total = H * maxT;
   const int lin = xcd_remap(blockIdx.x, total);
   if (lin >= total) return;
@@ -231,16 +237,17 @@ __global__ __launch_bounds__(256) void attn_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int jl = lane & 31, hh = lane >> 5;
 
-  // ---- runs of selected, non-empty key clusters (ascending cluster order)
+  // ---- runs of selected, non-empty key clusters (ascending cluster order);
+  //      thread tid owns clusters 4 tid .. 4 tid + 3
   const uint32_t* ur = unip + ((size_t)h * CQ + t) * (TA_CK / 32);
   const int32_t* ko = k_off + (size_t)h * (TA_CK + 1);
   const int32_t* kc = kcounts + (size_t)h * TA_CK;
+  const uint32_t nib = (ur[tid >> 3] >> (4 * (tid & 7))) & 0xfu;
+  int cnts[4];
   int nr = 0, ns = 0;
-  const uint32_t ubyte = (ur[tid >> 2] >> (8 * (tid & 3))) & 0xffu;  // clusters 8 tid .. 8 tid + 7
-  int cnts[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    cnts[j] = ((ubyte >> j) & 1u) ? kc[8 * tid + j] : 0;
+  for (int j = 0; j < 4; ++j) {
+    cnts[j] = ((nib >> j) & 1u) ? kc[4 * tid + j] : 0;
     nr += cnts[j] > 0;
     ns += cnts[j];
   }
@@ -250,17 +257,20 @@ __global__ __launch_bounds__(256) void attn_kernel(
     wsr[wave] = is;
   }
   __syncthreads();
-  int r = ir - nr, p = is - ns;
-  for (int i = 0; i < wave; ++i) {
-    r += wsc[i];
-    p += wsr[i];
-  }
-  const int nrun = wsc[0] + wsc[1] + wsc[2] + wsc[3];
-  const int kvlen = wsr[0] + wsr[1] + wsr[2] + wsr[3];
+  int r = ir - nr, p = is - ns, nrun = 0, kvlen = 0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int i = 0; i < TA_WAVES; ++i) {
+    if (i < wave) {
+      r += wsc[i];
+      p += wsr[i];
+    }
+    nrun += wsc[i];
+    kvlen += wsr[i];
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
     if (cnts[j] > 0) {
-      runStart[r] = ko[8 * tid + j];
+      runStart[r] = ko[4 * tid + j];
       runCum[r] = p;
       ++r;
       p += cnts[j];
@@ -268,7 +278,7 @@ __global__ __launch_bounds__(256) void attn_kernel(
   }
   if (tid == 0) runCum[nrun] = kvlen;
 
-  const int qrow = wave * 32 + jl;         // query row inside the task
+  const int qrow = wave * 32 + jl;  // query row inside the task
   const bool qok = qrow < qrows;
   const bool wave_active = wave * 32 < qrows;
   const size_t obase = (size_t)h * N + qs;  // sorted-order output rows
@@ -290,37 +300,39 @@ __global__ __launch_bounds__(256) void attn_kernel(
   }
   __syncthreads();  // runs visible
 
-  // ---- loader mapping: 4 keys x 8 dims per thread
+  // ---- loader: thread = 2 keys (2 kq, 2 kq + 1) x 8 dims (dseg)
   const int kq = tid >> 4, dseg = tid & 15;
   const uint16_t* kbase = kp + (size_t)h * N * TA_D + 8 * dseg;
   const uint16_t* vbase = vp + (size_t)h * N * TA_D + 8 * dseg;
   int cur = 0;
-  u32x4 ldk[4], ldv[4];
+  u32x4 ldk0, ldk1, ldv0, ldv1;
+  auto row_of = [&](int pos) -> size_t {
+    while (runCum[cur + 1] <= pos) ++cur;
+    return (size_t)(runStart[cur] + pos - runCum[cur]);
+  };
   auto issue = [&](int tile) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int pos = tile * TA_KT + 4 * kq + i;
-      if (pos < kvlen) {
-        while (runCum[cur + 1] <= pos) ++cur;
-        const size_t row = (size_t)(runStart[cur] + pos - runCum[cur]);
-        ldk[i] = *(const u32x4*)(kbase + row * TA_D);
-        ldv[i] = *(const u32x4*)(vbase + row * TA_D);
-      } else {
-        ldk[i] = u32x4{0u, 0u, 0u, 0u};
-        ldv[i] = u32x4{0u, 0u, 0u, 0u};
-      }
+    const int p0 = tile * TA_KT + 2 * kq;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    ldk0 = z; ldv0 = z; ldk1 = z; ldv1 = z;
+    if (p0 < kvlen) {
+      const size_t r0 = row_of(p0);
+      ldk0 = *(const u32x4*)(kbase + r0 * TA_D);
+      ldv0 = *(const u32x4*)(vbase + r0 * TA_D);
+    }
+    if (p0 + 1 < kvlen) {
+      const size_t r1 = row_of(p0 + 1);
+      ldk1 = *(const u32x4*)(kbase + r1 * TA_D);
+      ldv1 = *(const u32x4*)(vbase + r1 * TA_D);
     }
   };
-  auto stash = [&]() {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *(u32x4*)(sK + (4 * kq + i) * TA_KP + 8 * dseg) = ldk[i];
+  auto stash = [&](int buf) {
+    *(u32x4*)(sK[buf] + (2 * kq) * TA_KP + 8 * dseg) = ldk0;
+    *(u32x4*)(sK[buf] + (2 * kq + 1) * TA_KP + 8 * dseg) = ldk1;
+    uint16_t* vt = sVt[buf] + (8 * dseg) * TA_VP + 2 * kq;
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       const int w = d >> 1, sh = (d & 1) * 16;
-      u32x2 v;
-      v[0] = ((ldv[0][w] >> sh) & 0xffffu) | (((ldv[1][w] >> sh) & 0xffffu) << 16);
-      v[1] = ((ldv[2][w] >> sh) & 0xffffu) | (((ldv[3][w] >> sh) & 0xffffu) << 16);
-      *(u32x2*)(sVt + (8 * dseg + d) * TA_VP + 4 * kq) = v;
+      *(uint32_t*)(vt + d * TA_VP) = ((ldv0[w] >> sh) & 0xffffu) | (((ldv1[w] >> sh) & 0xffffu) << 16);
     }
   };
 
@@ -332,10 +344,11 @@ __global__ __launch_bounds__(256) void attn_kernel(
 
   const int ntile = (kvlen + TA_KT - 1) / TA_KT;
   issue(0);
+  stash(0);
+  if (ntile > 1) issue(1);
+  __syncthreads();
   for (int tile = 0; tile < ntile; ++tile) {
-    stash();
-    __syncthreads();
-    if (tile + 1 < ntile) issue(tile + 1);
+    const int buf = tile & 1;
     if (wave_active) {
       // S^T block kb: keys 32 kb + 8 (a / 4) + 4 hh + a % 4 for query jl
       f32x16 S[2];
@@ -344,7 +357,7 @@ __global__ __launch_bounds__(256) void attn_kernel(
         S[kb] = zero16();
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-          const u32x4 a = *(const u32x4*)(sK + (32 * kb + jl) * TA_KP + 16 * s + 8 * hh);
+          const u32x4 a = *(const u32x4*)(sK[buf] + (32 * kb + jl) * TA_KP + 16 * s + 8 * hh);
           S[kb] = Mfma<T>::run(a, qb[s], S[kb]);
         }
       }
@@ -355,35 +368,38 @@ __global__ __launch_bounds__(256) void attn_kernel(
 #pragma unroll
         for (int a = 0; a < 16; ++a) {
           const int key = 32 * kb + 8 * (a / 4) + 4 * hh + (a % 4);
-          if (key >= valid) S[kb][a] = -__builtin_inff();
-          mx = fmaxf(mx, S[kb][a]);
+          const float sv = key < valid ? S[kb][a] * c : -__builtin_inff();
+          S[kb][a] = sv;
+          mx = fmaxf(mx, sv);
         }
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(m, mx * c);
-      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-      m = mnew;
+      // lazy max: move only when exceeded, then with headroom
+      if (__ballot(mx > m)) {
+        const float mnew = mx > m ? mx + TA_MARGIN : m;
+        const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+        m = mnew;
+        lsum *= alpha;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+          for (int a = 0; a < 16; ++a) O[nb][a] *= alpha;
+      }
       float ps = 0.f;
       u32x4 pb[4];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int a = 0; a < 16; a += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(S[kb][a], c, -mnew));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(S[kb][a + 1], c, -mnew));
+          const float p0 = __builtin_amdgcn_exp2f(S[kb][a] - m);
+          const float p1 = __builtin_amdgcn_exp2f(S[kb][a + 1] - m);
           ps += p0 + p1;
           pb[2 * kb + a / 8][(a % 8) / 2] = pack2(T::from_f(p0), T::from_f(p1));
         }
-      lsum = lsum * alpha + ps;
-      if (alpha != 1.0f) {
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-          for (int a = 0; a < 16; ++a) O[nb][a] *= alpha;
-      }
+      lsum += ps;
       // O^T[dim][query] += V^T[dim][keys] P^T[keys][query]
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
-        const uint16_t* vr = sVt + (32 * nb + jl) * TA_VP + 4 * hh;
+        const uint16_t* vr = sVt[buf] + (32 * nb + jl) * TA_VP + 4 * hh;
 #pragma unroll
         for (int mm = 0; mm < 4; ++mm) {
           const u32x2 lo = *(const u32x2*)(vr + 16 * mm);
@@ -393,6 +409,8 @@ __global__ __launch_bounds__(256) void attn_kernel(
         }
       }
     }
+    if (tile + 1 < ntile) stash(buf ^ 1);
+    if (tile + 2 < ntile) issue(tile + 2);
     __syncthreads();
   }
   if (!qok) return;
@@ -417,7 +435,7 @@ static void launch_attn(const void* q, const void* kp, const void* vp, const int
                         void* attn_out, float* lse, int H, int N, int CQ, hipStream_t st) {
   const int total = H * p.maxT;
   const int grid = ((total + 7) / 8) * 8;
-  hipLaunchKernelGGL(attn_kernel<T>, dim3(grid), dim3(256), 0, st, (const uint16_t*)q,
+  hipLaunchKernelGGL(attn_kernel<T>, dim3(grid), dim3(TA_WAVES * 64), 0, st, (const uint16_t*)q,
                      (const uint16_t*)kp, (const uint16_t*)vp, (const uint32_t*)unip, qperm,
                      kcounts, p.k_off, p.ntask, p.tasks, (uint16_t*)attn_out, lse, H, N, CQ,
                      p.maxT);

@@ -202,7 +202,7 @@ def tile_plan(qcounts, kcounts, unip, N, plan=None, stream=None):
 
 def plan_views(plan, H, N, CQ):
     """Named views of a plan buffer (k_off, kvlen, ntask, tasks)."""
-    maxT = CQ + (N + 127) // 128 + 1
+    maxT = CQ + (N + 255) // 256 + 1
     o = 0
     k_off = plan[o:o + H * 2049].view(H, 2049); o += H * 2049
     kvlen = plan[o:o + H * CQ].view(H, CQ); o += H * CQ
