@@ -264,7 +264,7 @@ def test_plan(dev):
         tasks = pv["tasks"][h, :nt]
         covered = np.zeros(N, dtype=int)
         for t, s, rows, _ in tasks:
-            assert 1 <= rows <= 256 and qoff[h, t] <= s and s + rows <= qoff[h, t] + qcounts[h, t]
+            assert 1 <= rows <= 128 and qoff[h, t] <= s and s + rows <= qoff[h, t] + qcounts[h, t]
             covered[s:s + rows] += 1
         assert np.all(covered == 1)
         work = tasks[:, 2].astype(np.int64) * kvlen[h, tasks[:, 0]]
@@ -339,3 +339,31 @@ def test_tail_merge(dev, dtype):
     got = c(out.float())
     tol = 5e-3 if dtype == torch.float16 else 3e-2
     assert np.abs(got - eo).max() < tol * max(1.0, np.abs(eo).max())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_attention_tail_matches_oracle(dev, dtype):
+    """run_planned (exact attention + residual + merge in one kernel) against
+    the oracle's S5 followed by S6, including empty and full unions."""
+    from token2tile_amd import ops
+    rng = np.random.default_rng(12)
+    q, k, v, kperm, kcounts, qlab, qperm, qcounts, unip, kp, vp = attn_case(rng, density=0.05)
+    H, N, _ = q.shape
+    QU = rng.normal(0, 1, (H, N, 32)).astype(np.float16)
+    cks = (rng.normal(0, 1, (H, 2048, 32)) * 0.3).astype(np.float16)
+    sumv = rng.normal(0, 1, (H, 2048, 128)).astype(np.float16)
+    lam = np.array([1.0, 3.0], dtype=np.float32)
+    tq, tkp, tvp = (g(a, dev).to(dtype) for a in (q, kp, vp))
+    out = torch.empty_like(tq)
+    plan = torch.empty(ops.plan_ints(H, N, qcounts.shape[1]), dtype=torch.int32, device=dev)
+    ops.tile_attn_run_planned(tq, tkp, tvp, g(qcounts, dev), g(kcounts, dev), g(unip, dev),
+                              g(QU, dev), g(cks, dev), g(sumv, dev), g(lam, dev), g(qlab, dev),
+                              g(qperm, dev), torch.tensor(1.0, device=dev), out, plan, True)
+    qf, kpf, vpf = (c(t.float()) for t in (tq, tkp, tvp))
+    ao, lse = O.tile_attention(qf, kpf, vpf, qcounts, kcounts, unip, qperm)
+    eo = O.tail_merge(ao, lse, QU, cks, sumv, kcounts, unip, qlab, qperm, lam, 1.0)
+    got = c(out.float())
+    tol = 5e-3 if dtype == torch.float16 else 2e-2
+    assert np.abs(got - eo).max() < tol
+    a, b = got.ravel().astype(np.float64), eo.ravel()
+    assert a @ b / (np.linalg.norm(a) * np.linalg.norm(b)) > 0.9999

@@ -77,6 +77,32 @@ template <> struct Mfma<BF16T> {
   }
 };
 
+// Two floats -> one packed pair of T (round to nearest even, one
+// v_cvt_pk_* instruction), and the sum of a packed pair added to acc (dot2
+// with (1, 1), fp32 accumulation).
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+template <typename T> struct Pk;
+template <> struct Pk<F16T> {
+  __device__ static inline uint32_t pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+  }
+  __device__ static inline float sum2(uint32_t p, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p), (f16x2){(_Float16)1.0f, (_Float16)1.0f},
+                                  acc, false);
+  }
+};
+template <> struct Pk<BF16T> {
+  __device__ static inline uint32_t pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+  }
+  __device__ static inline float sum2(uint32_t p, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p),
+                                           (bf16x2){(__bf16)1.0f, (__bf16)1.0f}, acc, false);
+  }
+};
+
 __device__ inline f32x16 zero16() {
   f32x16 z;
 #pragma unroll

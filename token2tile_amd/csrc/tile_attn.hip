@@ -17,14 +17,14 @@
 // the 2048 centroids (K = cks, V = sumv), masked by the query's union,
 // followed by the merge with the exact part.
 #include "t2t_common.h"
+#include <type_traits>
 
 #define TA_D 128
 #define TA_CK 2048
-#define TA_QT 256   // queries per task (8 waves x 32)
-#define TA_WAVES 8
+#define TA_QT 128   // queries per task (4 waves x 32)
+#define TA_WAVES 4
 #define TA_KT 64    // keys per tile
-#define TA_KP 136   // sK pitch (halves)
-#define TA_VP 68    // sVt pitch (halves)
+#define TA_VP 68    // residual-only sVt pitch (halves) of the unfused tail kernel
 
 // ---------------------------------------------------------------------------
 // plan layout (int32): k_off [H][2049] | kvlen [H][CQ] | ntask [H] |
@@ -212,20 +212,56 @@ __device__ inline int xcd_remap(int bid, int total) {
   return (bid % 8) * per + bid / 8;
 }
 
-#define TA_MARGIN 3.0f  // log2 units of headroom when the running max advances
+#define TA_MARGIN 3.0f   // log2 units of headroom when the exact-part max advances
+#define TL_MARGIN 2.0f   // natural-log units of headroom for the residual max
+#define TL_CT 64         // centroids per residual tile
+#define TL_CP 40         // residual centroid tile pitch (halves)
 
-template <typename T>
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+// LDS tile layouts (no padding, XOR swizzles keep the MFMA operand reads
+// conflict free):
+//   sK  [64 keys][128 dims]: 16-byte chunk c of row r lives at chunk c ^ (r & 15)
+//   sVt [128 dims][64 keys]: the 4-key granules a lane feeds to one MFMA
+//     (g = 4 m + h and 4 m + 2 + h) are stored side by side, so the operand is
+//     one 16-byte read: granule g sits in 16-byte unit (g & ~3) / 2 + (g & 1),
+//     half (g >> 1) & 1, and the unit is XOR-swizzled by ((d >> 1) ^ (d >> 4)) & 7
+__device__ inline int sk_off(int row, int chunk) { return row * 128 + 8 * (chunk ^ (row & 15)); }
+__device__ inline int vt_swz(int dim) { return ((dim >> 1) ^ (dim >> 4)) & 7; }
+__device__ inline int vt_unit_off(int dim, int unit) { return dim * 64 + 8 * (unit ^ vt_swz(dim)); }
+__device__ inline int vt_gran_off(int dim, int g) {
+  return vt_unit_off(dim, ((g & ~3) >> 1) + (g & 1)) + 4 * ((g >> 1) & 1);
+}
+
+__device__ inline float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+// (b.lo16 << 16) | a.lo16 and (b.hi16 << 16) | a.hi16
+__device__ inline uint32_t pack_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ inline uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+// keeps the compiler from if-converting a rarely taken block into selects
+#define T2T_REAL_BRANCH() asm volatile("" ::: "memory")
+
+// One work-group (4 waves, 32 queries each) per task of <= 128 queries, two
+// work-groups per CU.  FUSE = false: exact attention only, attn_out and lse
+// (log2 units) in sorted order.  FUSE = true: exact attention, then the
+// residual over the centroids outside the task's (shared) union and the
+// merge under one softmax, written at the original rows.
+template <typename T, bool FUSE>
 __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kp,
     const uint16_t* __restrict__ vp, const uint32_t* __restrict__ unip,
     const int32_t* __restrict__ qperm, const int32_t* __restrict__ kcounts,
     const int32_t* __restrict__ k_off, const int32_t* __restrict__ ntask,
-    const int32_t* __restrict__ tasks, uint16_t* __restrict__ out, float* __restrict__ lse,
-    int H, int N, int CQ, int maxT) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][TA_KT * TA_KP];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[2][TA_D * TA_VP];
-  __shared__ int runStart[TA_CK];
+    const int32_t* __restrict__ tasks, uint16_t* __restrict__ attn_out, float* __restrict__ lse,
+    const uint16_t* __restrict__ QU, const uint16_t* __restrict__ cks,
+    const uint16_t* __restrict__ sumv, const float* __restrict__ lam,
+    const float* __restrict__ tailw, uint16_t* __restrict__ out, int H, int N, int CQ, int maxT) {
+  __shared__ __attribute__((aligned(1024))) uint16_t sK[2][TA_KT * 128];
+  __shared__ __attribute__((aligned(16))) uint16_t sVt[2][TA_D * 64];
+  __shared__ uint16_t runCl[TA_CK];
   __shared__ int runCum[TA_CK + 1];
+  __shared__ int sIdx[2][TA_KT];
+  __shared__ __attribute__((aligned(16))) float sCnt[2][TL_CT];
   __shared__ int wsc[TA_WAVES], wsr[TA_WAVES];
   const int total = H * maxT;
   const int lin = xcd_remap(blockIdx.x, total);
@@ -238,16 +274,16 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
   const int jl = lane & 31, hh = lane >> 5;
 
   // ---- runs of selected, non-empty key clusters (ascending cluster order);
-  //      thread tid owns clusters 4 tid .. 4 tid + 3
+  //      thread tid owns clusters 8 tid .. 8 tid + 7
   const uint32_t* ur = unip + ((size_t)h * CQ + t) * (TA_CK / 32);
   const int32_t* ko = k_off + (size_t)h * (TA_CK + 1);
   const int32_t* kc = kcounts + (size_t)h * TA_CK;
-  const uint32_t nib = (ur[tid >> 3] >> (4 * (tid & 7))) & 0xfu;
-  int cnts[4];
+  const uint32_t byte = (ur[tid >> 2] >> (8 * (tid & 3))) & 0xffu;
+  int cnts[8];
   int nr = 0, ns = 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    cnts[j] = ((nib >> j) & 1u) ? kc[4 * tid + j] : 0;
+  for (int j = 0; j < 8; ++j) {
+    cnts[j] = ((byte >> j) & 1u) ? kc[8 * tid + j] : 0;
     nr += cnts[j] > 0;
     ns += cnts[j];
   }
@@ -268,9 +304,9 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     kvlen += wsr[i];
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < 8; ++j) {
     if (cnts[j] > 0) {
-      runStart[r] = ko[4 * tid + j];
+      runCl[r] = (uint16_t)(8 * tid + j);
       runCum[r] = p;
       ++r;
       p += cnts[j];
@@ -281,59 +317,37 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
   const int qrow = wave * 32 + jl;  // query row inside the task
   const bool qok = qrow < qrows;
   const bool wave_active = wave * 32 < qrows;
-  const size_t obase = (size_t)h * N + qs;  // sorted-order output rows
-  if (kvlen == 0) {
-    if (qok) {
-      uint16_t* o = out + (obase + qrow) * TA_D + 64 * hh;
-      for (int i = 0; i < 64; i += 8) *(u32x4*)(o + i) = u32x4{0u, 0u, 0u, 0u};
-      if (hh == 0) lse[obase + qrow] = -__builtin_inff();
-    }
-    return;
-  }
-  // ---- queries: B operand fragments (dims 16 s + 8 hh .. + 7)
-  u32x4 qb[8];
-  {
-    const int orig = qperm[(size_t)h * N + qs + (qok ? qrow : 0)];
-    const uint16_t* qr = q + ((size_t)h * N + orig) * TA_D + 8 * hh;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) qb[s] = *(const u32x4*)(qr + 16 * s);
-  }
-  __syncthreads();  // runs visible
+  const size_t obase = (size_t)h * N + qs;  // sorted-order rows of the task
+  const int orig = qperm[obase + (qok ? qrow : 0)];
+  const int kq = tid >> 4, dseg = tid & 15;  // V loader: 4 keys (4 kq ..) x 8 dims (dseg)
 
-  // ---- loader: thread = 2 keys (2 kq, 2 kq + 1) x 8 dims (dseg)
-  const int kq = tid >> 4, dseg = tid & 15;
-  const uint16_t* kbase = kp + (size_t)h * N * TA_D + 8 * dseg;
-  const uint16_t* vbase = vp + (size_t)h * N * TA_D + 8 * dseg;
-  int cur = 0;
-  u32x4 ldk0, ldk1, ldv0, ldv1;
-  auto row_of = [&](int pos) -> size_t {
-    while (runCum[cur + 1] <= pos) ++cur;
-    return (size_t)(runStart[cur] + pos - runCum[cur]);
-  };
-  auto issue = [&](int tile) {
-    const int p0 = tile * TA_KT + 2 * kq;
-    const u32x4 z = {0u, 0u, 0u, 0u};
-    ldk0 = z; ldv0 = z; ldk1 = z; ldv1 = z;
-    if (p0 < kvlen) {
-      const size_t r0 = row_of(p0);
-      ldk0 = *(const u32x4*)(kbase + r0 * TA_D);
-      ldv0 = *(const u32x4*)(vbase + r0 * TA_D);
-    }
-    if (p0 + 1 < kvlen) {
-      const size_t r1 = row_of(p0 + 1);
-      ldk1 = *(const u32x4*)(kbase + r1 * TA_D);
-      ldv1 = *(const u32x4*)(vbase + r1 * TA_D);
-    }
-  };
-  auto stash = [&](int buf) {
-    *(u32x4*)(sK[buf] + (2 * kq) * TA_KP + 8 * dseg) = ldk0;
-    *(u32x4*)(sK[buf] + (2 * kq + 1) * TA_KP + 8 * dseg) = ldk1;
-    uint16_t* vt = sVt[buf] + (8 * dseg) * TA_VP + 2 * kq;
+  // ---- stage 4 rows x 8 dims into the transposed, swizzled sVt[buf]
+  auto stash_vt = [&](int buf, const u32x4 (&v)[4]) {
 #pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      const int w = d >> 1, sh = (d & 1) * 16;
-      *(uint32_t*)(vt + d * TA_VP) = ((ldv0[w] >> sh) & 0xffffu) | (((ldv1[w] >> sh) & 0xffffu) << 16);
+    for (int w = 0; w < 4; ++w) {
+      const u32x2 lo = {pack_lo(v[0][w], v[1][w]), pack_lo(v[2][w], v[3][w])};
+      const u32x2 hi = {pack_hi(v[0][w], v[1][w]), pack_hi(v[2][w], v[3][w])};
+      *(u32x2*)(sVt[buf] + vt_gran_off(8 * dseg + 2 * w, kq)) = lo;
+      *(u32x2*)(sVt[buf] + vt_gran_off(8 * dseg + 2 * w + 1, kq)) = hi;
     }
+  };
+  // ---- O^T += V^T P^T over one 64-key tile
+  auto pv = [&](f32x16 (&Oa)[4], int buf, const u32x4 (&pb)[4], auto mf) {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int dim = 32 * nb + jl;
+#pragma unroll
+      for (int mm = 0; mm < 4; ++mm) {
+        const u32x4 a = *(const u32x4*)(sVt[buf] + vt_unit_off(dim, 2 * mm + hh));
+        Oa[nb] = mf(a, pb[mm], Oa[nb]);
+      }
+    }
+  };
+  auto rescale = [&](f32x16 (&Oa)[4], float alpha) {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int a = 0; a < 16; ++a) Oa[nb][a] *= alpha;
   };
 
   const float c = 0.08838834764831845f * 1.4426950408889634f;  // 1/sqrt(128) * log2(e)
@@ -342,103 +356,305 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) O[nb] = zero16();
 
-  const int ntile = (kvlen + TA_KT - 1) / TA_KT;
-  issue(0);
-  stash(0);
-  if (ntile > 1) issue(1);
-  __syncthreads();
-  for (int tile = 0; tile < ntile; ++tile) {
-    const int buf = tile & 1;
-    if (wave_active) {
-      // S^T block kb: keys 32 kb + 8 (a / 4) + 4 hh + a % 4 for query jl
+  if (kvlen > 0) {
+    // ---- queries: B operand fragments (dims 16 s + 8 hh .. + 7)
+    u32x4 qb[8];
+    {
+      const uint16_t* qr = q + ((size_t)h * N + orig) * TA_D + 8 * hh;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) qb[s] = *(const u32x4*)(qr + 16 * s);
+    }
+    const char* kh = (const char*)(kp + (size_t)h * N * TA_D);
+    const char* vh = (const char*)(vp + (size_t)h * N * TA_D) + 16 * dseg;
+    const int ntile = (kvlen + TA_KT - 1) / TA_KT;
+    int cur = 0;  // run cursor of the index builders (threads 0..63)
+    // source rows of tile `tile` -> sIdx[tile & 1]; past the end -> row 0
+    // (its keys are masked and its values multiply a zero probability)
+    auto build_idx = [&](int tile) {
+      if (tid < TA_KT) {
+        const int pos = tile * TA_KT + tid;
+        int row = 0;
+        if (pos < kvlen) {
+          while (runCum[cur + 1] <= pos) ++cur;
+          row = ko[runCl[cur]] + pos - runCum[cur];
+        }
+        sIdx[tile & 1][tid] = row;
+      }
+    };
+    u32x4 ldv[4];
+    // K tile via LDS DMA (each wave instruction fills 4 whole rows, the lane
+    // fetching the chunk that belongs at its swizzled position), V tile into
+    // registers for the transposed store
+    auto issue = [&](int tile) {
+      const int buf = tile & 1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int blk = 4 * i + wave;
+        const int row = 4 * blk + (lane >> 4);
+        const uint32_t off = (uint32_t)sIdx[buf][row] * 256u + 16u * ((lane & 15) ^ (row & 15));
+        __builtin_amdgcn_global_load_lds((const glb_void_t*)(kh + off),
+                                         (lds_void_t*)(sK[buf] + blk * 4 * 128), 16, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        ldv[i] = *(const u32x4*)(vh + (uint32_t)sIdx[buf][4 * kq + i] * 256u);
+    };
+    // one 64-key tile of the online softmax; MASK: the last, partial tile
+    auto tile_step = [&](int buf, int valid, auto MASK) {
       f32x16 S[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         S[kb] = zero16();
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-          const u32x4 a = *(const u32x4*)(sK[buf] + (32 * kb + jl) * TA_KP + 16 * s + 8 * hh);
+          const u32x4 a = *(const u32x4*)(sK[buf] + sk_off(32 * kb + jl, 2 * s + hh));
           S[kb] = Mfma<T>::run(a, qb[s], S[kb]);
         }
       }
-      const int valid = kvlen - tile * TA_KT;
-      float mx = -__builtin_inff();
+      if constexpr (decltype(MASK)::value) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int a = 0; a < 16; ++a)
+            if (32 * kb + 8 * (a / 4) + 4 * hh + (a % 4) >= valid) S[kb][a] = -__builtin_inff();
+      }
+      float mr = -__builtin_inff();
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int a = 0; a < 16; ++a) {
-          const int key = 32 * kb + 8 * (a / 4) + 4 * hh + (a % 4);
-          const float sv = key < valid ? S[kb][a] * c : -__builtin_inff();
-          S[kb][a] = sv;
-          mx = fmaxf(mx, sv);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        for (int a = 0; a < 16; a += 2) mr = vmax(mr, vmax(S[kb][a], S[kb][a + 1]));
+      mr = vmax(mr, __shfl_xor(mr, 32, 64));
+      const float mx = mr * c;
       // lazy max: move only when exceeded, then with headroom
-      if (__ballot(mx > m)) {
+      if (__builtin_amdgcn_readfirstlane((int)(__ballot(mx > m) != 0ull))) {
+        T2T_REAL_BRANCH();
         const float mnew = mx > m ? mx + TA_MARGIN : m;
         const float alpha = __builtin_amdgcn_exp2f(m - mnew);
         m = mnew;
         lsum *= alpha;
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-          for (int a = 0; a < 16; ++a) O[nb][a] *= alpha;
+        rescale(O, alpha);
       }
-      float ps = 0.f;
+      const float nm = -m;
       u32x4 pb[4];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int a = 0; a < 16; a += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(S[kb][a] - m);
-          const float p1 = __builtin_amdgcn_exp2f(S[kb][a + 1] - m);
-          ps += p0 + p1;
-          pb[2 * kb + a / 8][(a % 8) / 2] = pack2(T::from_f(p0), T::from_f(p1));
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(S[kb][a], c, nm));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(S[kb][a + 1], c, nm));
+          const uint32_t pk = Pk<T>::pack(p0, p1);
+          lsum = Pk<T>::sum2(pk, lsum);
+          pb[2 * kb + a / 8][(a % 8) / 2] = pk;
         }
-      lsum += ps;
-      // O^T[dim][query] += V^T[dim][keys] P^T[keys][query]
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        const uint16_t* vr = sVt[buf] + (32 * nb + jl) * TA_VP + 4 * hh;
-#pragma unroll
-        for (int mm = 0; mm < 4; ++mm) {
-          const u32x2 lo = *(const u32x2*)(vr + 16 * mm);
-          const u32x2 hi = *(const u32x2*)(vr + 16 * mm + 8);
-          const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-          O[nb] = Mfma<T>::run(a, pb[mm], O[nb]);
-        }
-      }
-    }
-    if (tile + 1 < ntile) stash(buf ^ 1);
-    if (tile + 2 < ntile) issue(tile + 2);
+      pv(O, buf, pb, [](const u32x4& a_, const u32x4& b_, const f32x16& c_) {
+        return Mfma<T>::run(a_, b_, c_);
+      });
+    };
+    __syncthreads();  // runs visible
+    build_idx(0);
+    if (ntile > 1) build_idx(1);
     __syncthreads();
-  }
-  if (!qok) return;
-  const float lt = lsum + __shfl_xor(lsum, 32, 64);
-  const float inv = 1.0f / lt;
-  uint16_t* orow = out + (obase + qrow) * TA_D;
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      u32x2 v;
-      v[0] = pack2(T::from_f(O[nb][4 * g] * inv), T::from_f(O[nb][4 * g + 1] * inv));
-      v[1] = pack2(T::from_f(O[nb][4 * g + 2] * inv), T::from_f(O[nb][4 * g + 3] * inv));
-      *(u32x2*)(orow + 32 * nb + 8 * g + 4 * hh) = v;
+    issue(0);
+    stash_vt(0, ldv);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (ntile > 1) issue(1);
+    if (ntile > 2) build_idx(2);
+    // full tiles in the loop; a partial last tile is peeled after it (one
+    // masked copy of the tile body outside the loop keeps register pressure
+    // of the loop at that of the unmasked body)
+    const int nfull = (kvlen % TA_KT) ? ntile - 1 : ntile;
+    int tile = 0;
+    for (; tile < nfull; ++tile) {
+      const int buf = tile & 1;
+      if (wave_active) tile_step(buf, TA_KT, std::false_type{});
+      if (tile + 1 < ntile) stash_vt(buf ^ 1, ldv);
+      __builtin_amdgcn_s_waitcnt(0);  // K DMA of tile + 1 landed
+      __syncthreads();
+      if (tile + 2 < ntile) issue(tile + 2);
+      if (tile + 3 < ntile) build_idx(tile + 3);
     }
-  if (hh == 0) lse[obase + qrow] = m + __log2f(lt);
+    if (tile < ntile && wave_active) tile_step(tile & 1, kvlen - tile * TA_KT, std::true_type{});
+  }
+  const float lt = lsum + __shfl_xor(lsum, 32, 64);
+  const float inv = kvlen > 0 ? 1.0f / lt : 0.f;
+  const float lse2 = kvlen > 0 ? m + __log2f(lt) : -__builtin_inff();
+  // exact output of the lane's 64 dims, rounded to T as the exact buffer
+  // holds it: sorted-order attn_out (exact-only kernel) or, for the fused
+  // kernel, the original row of out, read back by the merge
+  if (qok) {
+    uint16_t* orow = FUSE ? out + ((size_t)h * N + orig) * TA_D : attn_out + (obase + qrow) * TA_D;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *(u32x2*)(orow + 32 * nb + 8 * g + 4 * hh) =
+            u32x2{Pk<T>::pack(O[nb][4 * g] * inv, O[nb][4 * g + 1] * inv),
+                  Pk<T>::pack(O[nb][4 * g + 2] * inv, O[nb][4 * g + 3] * inv)};
+  }
+  if constexpr (!FUSE) {
+    if (qok && hh == 0) lse[obase + qrow] = lse2;
+    return;
+  } else {
+    // ---------------- residual over the centroids outside the union ----------
+    // Centroids inside the union are staged with zero count and zero value
+    // sum, so they add nothing to phi or O and need no per-score test.
+    const float L2E = 1.4426950408889634f;
+    uint32_t todo = 0;  // centroid tiles not entirely inside the union
+#pragma unroll 1
+    for (int tc = 0; tc < TA_CK / TL_CT; ++tc)
+      if ((ur[2 * tc] & ur[2 * tc + 1]) != 0xffffffffu) todo |= 1u << tc;
+    u32x4 qu0, qu1;
+    {
+      const uint16_t* qr = QU + ((size_t)h * N + orig) * 32 + 8 * hh;
+      qu0 = *(const u32x4*)(qr);
+      qu1 = *(const u32x4*)(qr + 16);
+    }
+    const uint16_t* chh = cks + (size_t)h * TA_CK * 32;
+    const uint16_t* shh = sumv + (size_t)h * TA_CK * TA_D + 8 * dseg;
+    u32x4 lc, lv[4];
+    float lcnt = 0.f;
+    auto issue_r = [&](int tc) {
+      lc = *(const u32x4*)(chh + (size_t)(tc * TL_CT + (tid >> 2)) * 32 + 8 * (tid & 3));
+      const uint32_t w4 = (ur[2 * tc + (kq >> 3)] >> (4 * (kq & 7))) & 0xfu;  // my 4 centroids
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        lv[i] = *(const u32x4*)(shh + (size_t)(tc * TL_CT + 4 * kq + i) * TA_D);
+        if ((w4 >> i) & 1u) lv[i] = u32x4{0u, 0u, 0u, 0u};
+      }
+      if (tid < TL_CT)
+        lcnt = ((ur[2 * tc + (tid >> 5)] >> (tid & 31)) & 1u) ? 0.f : (float)kc[tc * TL_CT + tid];
+    };
+    auto stash_r = [&](int buf) {
+      *(u32x4*)(sK[buf] + (tid >> 2) * TL_CP + 8 * (tid & 3)) = lc;
+      stash_vt(buf, lv);
+      if (tid < TL_CT) sCnt[buf][tid] = lcnt;
+    };
+    float m2 = -__builtin_inff(), phi = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) O[nb] = zero16();
+    __syncthreads();  // the exact loop's buffers are free
+    uint32_t rest = todo;
+    int tcur = rest ? __builtin_ctz(rest) : -1;
+    if (rest) rest &= rest - 1;
+    int tnext = rest ? __builtin_ctz(rest) : -1;
+    if (rest) rest &= rest - 1;
+    if (tcur >= 0) {
+      issue_r(tcur);
+      stash_r(0);
+      if (tnext >= 0) issue_r(tnext);
+    }
+    __syncthreads();
+    int buf = 0;
+    while (tcur >= 0) {
+      // scores of the lane's query against 32 kb + 8 (a / 4) + 4 hh + a % 4,
+      // rounded to fp16 as the selection's scores are
+      uint32_t sh[2][8];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const uint16_t* crow = sK[buf] + (32 * kb + jl) * TL_CP + 8 * hh;
+        f32x16 S = zero16();
+        S = Mfma<F16T>::run(*(const u32x4*)(crow), qu0, S);
+        S = Mfma<F16T>::run(*(const u32x4*)(crow + 16), qu1, S);
+#pragma unroll
+        for (int a = 0; a < 16; a += 2) sh[kb][a / 2] = Pk<F16T>::pack(S[a], S[a + 1]);
+      }
+      float sv[2][16];
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int a = 0; a < 16; a += 2) {
+          sv[kb][a] = h2f((uint16_t)(sh[kb][a / 2] & 0xffffu));
+          sv[kb][a + 1] = h2f((uint16_t)(sh[kb][a / 2] >> 16));
+          mx = vmax(mx, vmax(sv[kb][a], sv[kb][a + 1]));
+        }
+      mx = vmax(mx, __shfl_xor(mx, 32, 64));
+      if (__builtin_amdgcn_readfirstlane((int)(__ballot(mx > m2) != 0ull))) {
+        T2T_REAL_BRANCH();
+        const float mnew = mx > m2 ? mx + TL_MARGIN : m2;
+        const float alpha = __builtin_amdgcn_exp2f((m2 - mnew) * L2E);
+        m2 = mnew;
+        phi *= alpha;
+        rescale(O, alpha);
+      }
+      const float nm = -m2 * L2E;
+      u32x4 pb[4];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // counts of centroids 32 kb + 8 j + 4 hh .. + 3
+          const f32x4 cn = *(const f32x4*)(sCnt[buf] + 32 * kb + 8 * j + 4 * hh);
+          float pe[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pe[e] = __builtin_amdgcn_exp2f(fmaf(sv[kb][4 * j + e], L2E, nm));
+            phi = fmaf(pe[e], cn[e], phi);
+          }
+          pb[2 * kb + j / 2][2 * (j % 2)] = Pk<F16T>::pack(pe[0], pe[1]);
+          pb[2 * kb + j / 2][2 * (j % 2) + 1] = Pk<F16T>::pack(pe[2], pe[3]);
+        }
+      pv(O, buf, pb, [](const u32x4& a_, const u32x4& b_, const f32x16& c_) {
+        return Mfma<F16T>::run(a_, b_, c_);
+      });
+      if (tnext >= 0) stash_r(buf ^ 1);
+      const int tn2 = rest ? __builtin_ctz(rest) : -1;
+      if (rest) rest &= rest - 1;
+      __syncthreads();
+      if (tn2 >= 0) issue_r(tn2);
+      tcur = tnext;
+      tnext = tn2;
+      buf ^= 1;
+    }
+    if (!qok) return;
+    // ---------------- merge under one softmax --------------------------------
+    phi += __shfl_xor(phi, 32, 64);
+    const float tw = *tailw;
+    const float lm = lam[h];
+    const float le = lse2 * 0.6931471805599453f;
+    float ex, st;
+    if (le >= m2) {
+      ex = 1.0f;
+      st = __expf(m2 - le);
+    } else {
+      ex = __expf(le - m2);
+      st = 1.0f;
+    }
+    const float ph = st * phi;
+    const bool bad = ph <= 1.0e-6f * ex;
+    const float den = fmaxf(ex + ph * tw, 1.0e-12f);
+    const float wx = ex / den, wt = st * tw * lm / den;
+    if (bad) return;  // the exact part already written is the output
+    uint16_t* orow = out + ((size_t)h * N + orig) * TA_D;
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        u32x2 v = *(const u32x2*)(orow + 32 * nb + 8 * g + 4 * hh);  // exact part
+        const uint32_t w0 = v[0], w1 = v[1];
+        const float x0 = T::to_f((uint16_t)(w0 & 0xffff)), x1 = T::to_f((uint16_t)(w0 >> 16));
+        const float x2 = T::to_f((uint16_t)(w1 & 0xffff)), x3 = T::to_f((uint16_t)(w1 >> 16));
+        v[0] = Pk<T>::pack(fmaf(wt, O[nb][4 * g], wx * x0), fmaf(wt, O[nb][4 * g + 1], wx * x1));
+        v[1] = Pk<T>::pack(fmaf(wt, O[nb][4 * g + 2], wx * x2), fmaf(wt, O[nb][4 * g + 3], wx * x3));
+        *(u32x2*)(orow + 32 * nb + 8 * g + 4 * hh) = v;
+      }
+  }
 }
 
-template <typename T>
+template <typename T, bool FUSE>
 static void launch_attn(const void* q, const void* kp, const void* vp, const int32_t* unip,
                         const int32_t* qperm, const int32_t* kcounts, const PlanView& p,
-                        void* attn_out, float* lse, int H, int N, int CQ, hipStream_t st) {
+                        void* attn_out, float* lse, const void* QU, const void* cks,
+                        const void* sumv, const float* lam, const float* tailw, void* out, int H,
+                        int N, int CQ, hipStream_t st) {
   const int total = H * p.maxT;
   const int grid = ((total + 7) / 8) * 8;
-  hipLaunchKernelGGL(attn_kernel<T>, dim3(grid), dim3(TA_WAVES * 64), 0, st, (const uint16_t*)q,
-                     (const uint16_t*)kp, (const uint16_t*)vp, (const uint32_t*)unip, qperm,
-                     kcounts, p.k_off, p.ntask, p.tasks, (uint16_t*)attn_out, lse, H, N, CQ,
-                     p.maxT);
+  hipLaunchKernelGGL((attn_kernel<T, FUSE>), dim3(grid), dim3(TA_WAVES * 64), 0, st,
+                     (const uint16_t*)q, (const uint16_t*)kp, (const uint16_t*)vp,
+                     (const uint32_t*)unip, qperm, kcounts, p.k_off, p.ntask, p.tasks,
+                     (uint16_t*)attn_out, lse, (const uint16_t*)QU, (const uint16_t*)cks,
+                     (const uint16_t*)sumv, lam, tailw, (uint16_t*)out, H, N, CQ, p.maxT);
 }
 
 // ---------------------------------------------------------------------------
@@ -615,9 +831,11 @@ extern "C" int t2t_tile_attn_exact(const void* q, const void* kp, const void* vp
   PlanView p = plan_view((int32_t*)plan, H, N, CQ);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == T2T_F16)
-    launch_attn<F16T>(q, kp, vp, unip, qperm, kcounts, p, attn_out, lse, H, N, CQ, st);
+    launch_attn<F16T, false>(q, kp, vp, unip, qperm, kcounts, p, attn_out, lse, nullptr, nullptr,
+                             nullptr, nullptr, nullptr, nullptr, H, N, CQ, st);
   else
-    launch_attn<BF16T>(q, kp, vp, unip, qperm, kcounts, p, attn_out, lse, H, N, CQ, st);
+    launch_attn<BF16T, false>(q, kp, vp, unip, qperm, kcounts, p, attn_out, lse, nullptr, nullptr,
+                              nullptr, nullptr, nullptr, nullptr, H, N, CQ, st);
   T2T_LAUNCH_CHECK("tile_attn_exact");
   return T2T_OK;
 }
@@ -647,11 +865,10 @@ extern "C" int t2t_tail_merge(const void* attn_out, const float* lse, const void
 }
 
 extern "C" size_t t2t_tile_attn_ws_bytes(int H, int N, int dtype) {
+  (void)H;
+  (void)N;
   (void)dtype;
-  WsCarver w(nullptr);
-  w.take<uint16_t>((size_t)H * N * TA_D);
-  w.take<float>((size_t)H * N);
-  return w.off;
+  return 0;  // the fused kernel keeps the exact part in registers
 }
 
 extern "C" int t2t_tile_attn_run_planned(const void* q, const void* kp, const void* vp, int dtype,
@@ -661,19 +878,13 @@ extern "C" int t2t_tile_attn_run_planned(const void* q, const void* kp, const vo
                                          const int32_t* qperm, const float* tailw_dev, void* out,
                                          int32_t* plan, int rebuild_plan, int H, int N, int CQ,
                                          void* ws, size_t ws_bytes, void* stream) {
+  (void)ws;
+  (void)ws_bytes;
   T2T_REQUIRE(q && kp && vp && qcounts && kcounts && unip && QU && cks && sumv && lam && qlab &&
                   qperm && tailw_dev && out && plan,
               "tile_attn_run_planned: null pointer");
   T2T_REQUIRE(check_dtype(dtype), "tile_attn_run_planned: dtype %d", dtype);
   T2T_REQUIRE(H > 0 && N > 0 && CQ > 0, "tile_attn_run_planned: H=%d N=%d CQ=%d", H, N, CQ);
-  const size_t need = t2t_tile_attn_ws_bytes(H, N, dtype);
-  if (!ws || ws_bytes < need) {
-    t2t_set_error("tile_attn_run_planned: workspace %zu < %zu bytes", ws_bytes, need);
-    return T2T_ERR_WORKSPACE;
-  }
-  WsCarver w(ws);
-  uint16_t* ao = w.take<uint16_t>((size_t)H * N * TA_D);
-  float* lse = w.take<float>((size_t)H * N);
   hipStream_t st = (hipStream_t)stream;
   if (rebuild_plan) {
     const int rc = t2t_tile_plan(qcounts, kcounts, unip, plan, H, N, CQ, stream);
@@ -681,10 +892,11 @@ extern "C" int t2t_tile_attn_run_planned(const void* q, const void* kp, const vo
   }
   PlanView p = plan_view(plan, H, N, CQ);
   if (dtype == T2T_F16)
-    launch_attn<F16T>(q, kp, vp, unip, qperm, kcounts, p, ao, lse, H, N, CQ, st);
+    launch_attn<F16T, true>(q, kp, vp, unip, qperm, kcounts, p, nullptr, nullptr, QU, cks, sumv,
+                            lam, tailw_dev, out, H, N, CQ, st);
   else
-    launch_attn<BF16T>(q, kp, vp, unip, qperm, kcounts, p, ao, lse, H, N, CQ, st);
-  T2T_LAUNCH_CHECK("tile_attn");
-  return t2t_tail_merge(ao, lse, QU, cks, sumv, kcounts, unip, qlab, qperm, lam, tailw_dev, out,
-                        dtype, H, N, CQ, stream);
+    launch_attn<BF16T, true>(q, kp, vp, unip, qperm, kcounts, p, nullptr, nullptr, QU, cks, sumv,
+                             lam, tailw_dev, out, H, N, CQ, st);
+  T2T_LAUNCH_CHECK("tile_attn_run_planned");
+  return T2T_OK;
 }

@@ -13,10 +13,10 @@ the model dtype, accepted without a conversion pass):
   2. clustering   one warm-started k-means update            t2t_kmm_run
   3. scoring      gl = QU cks^T                              t2t_score
   4. selection    per-query budget prefix + cluster union    t2t_select_run_packed
-  5. attention    task plan, exact attention over the unions,
-                  residual over the other clusters, merge    t2t_tile_plan,
-                                                             t2t_tile_attn_exact,
-                                                             t2t_tail_merge
+  5. attention    task plan, then one fused kernel: exact
+                  attention over the unions, residual over
+                  the other clusters, merge                  t2t_tile_plan,
+                                                             t2t_tile_attn_run_planned
 
 The output is in the original row order.  With ``mask_refresh=R`` the
 structure (labels, permutations, sizes, centroids, union, task plan) is
@@ -212,8 +212,7 @@ class MaskedStepDeploy:
             io = dict(kp=torch.empty(H, N, D, device=self.dev, dtype=dtype),
                       vp=torch.empty(H, N, D, device=self.dev, dtype=dtype),
                       out=torch.empty(H, N, D, device=self.dev, dtype=dtype),
-                      attn_out=torch.empty(H, N, D, device=self.dev, dtype=dtype),
-                      lse=torch.empty(H, N, device=self.dev, dtype=torch.float32))
+                      attn_out=None, lse=None)
             self._io[dtype] = io
         return io
 
@@ -368,12 +367,9 @@ class MaskedStepDeploy:
                 with self._stage("plan"):
                     ops.tile_plan(tile_sizes, counts, unip, N, plan=plan, stream=s0)
             with self._stage("attention"):
-                ops.tile_attn_exact(q, io["kp"], io["vp"], counts, unip, qperm, plan,
-                                    attn_out=io["attn_out"], lse=io["lse"], stream=s0)
-            with self._stage("tail"):
-                ops.tail_merge(io["attn_out"], io["lse"], self.QU, cks, self._kmm_sumv,
-                               counts, unip, qlab_cur, qperm, self._kmm_lam, self.tailw_t,
-                               out=io["out"], stream=s0)
+                ops.tile_attn_run_planned(q, io["kp"], io["vp"], tile_sizes, counts, unip,
+                                          self.QU, cks, self._kmm_sumv, self._kmm_lam, qlab_cur,
+                                          qperm, self.tailw_t, io["out"], plan, False, stream=s0)
         s1.wait_stream(s0)
         cur = torch.cuda.current_stream(self.dev)
         cur.wait_stream(s0)

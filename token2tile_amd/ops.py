@@ -202,7 +202,7 @@ def tile_plan(qcounts, kcounts, unip, N, plan=None, stream=None):
 
 def plan_views(plan, H, N, CQ):
     """Named views of a plan buffer (k_off, kvlen, ntask, tasks)."""
-    maxT = CQ + (N + 255) // 256 + 1
+    maxT = CQ + (N + 127) // 128 + 1
     o = 0
     k_off = plan[o:o + H * 2049].view(H, 2049); o += H * 2049
     kvlen = plan[o:o + H * CQ].view(H, CQ); o += H * CQ
@@ -241,12 +241,9 @@ def tile_attn_run_planned(q, kp, vp, qcounts, kcounts, unip, QU, cks, sumv, lam,
                           tailw_t, out, plan, rebuild, ws=None, stream=None):
     H, N, D = q.shape
     CQ = qcounts.shape[1]
-    need = attn_ws_bytes(H, N, q.dtype)
-    if ws is None or ws.numel() < need:
-        ws = _ws(need, _dev(q))
     call("t2t_tile_attn_run_planned", q, kp, vp, dtype_code(q.dtype), qcounts, kcounts, unip, QU,
-         cks, sumv, lam, qlab, qperm, tailw_t, out, plan, int(bool(rebuild)), H, N, CQ, ws,
-         ws.numel(), stream_handle(stream))
+         cks, sumv, lam, qlab, qperm, tailw_t, out, plan, int(bool(rebuild)), H, N, CQ, None, 0,
+         stream_handle(stream))
     return out
 
 
