@@ -148,7 +148,7 @@ def test_sanitize_state():
 # ---------------------------------------------------------------------------
 def _manual_meta(step, cache, **kw):
     return _meta(step_index=step, cache=cache, profile_name="manual", ns_base=300,
-                 dense_prefix_steps=2, cq=32, ck=256, step_profile=(1.0, 1.0, 1.0, 1.0),
+                 dense_prefix_steps=2, cq=32, ck=2048, step_profile=(1.0, 1.0, 1.0, 1.0),
                  layer_profile=(1.0,) * 6, cfg_mult=(1.0, 0.75), **kw)
 
 
@@ -173,7 +173,7 @@ def test_backend_forward_matches_operator(dev):
         impl.forward(*qkv, _manual_meta(2, cache))
 
     # the same sequence straight through the operator
-    op = deploy_step.MaskedStepDeploy(H, N, 32, C=256, D=D, s_frac=300 / N, mask_refresh=4,
+    op = deploy_step.MaskedStepDeploy(H, N, 32, C=2048, D=D, s_frac=300 / N, mask_refresh=4,
                                       cfg_reuse=True, device=dev)
     q, k, v = (t[0].transpose(0, 1).contiguous() for t in qkv)
     states = {}

@@ -10,8 +10,8 @@ def test_loaders_expose_reference_methods():
     kmm = ext_compat.KmmExt()
     sel = ext_compat.SelectUnionExt()
     att = ext_compat.TileAttnExt()
-    for obj, names in ((kmm, ("run", "run_vstats_gather")),
-                       (sel, ("run", "run_packed", "run_split_packed")),
+    for obj, names in ((kmm, ("run", "run_vstats", "run_vstats_gather")),
+                       (sel, ("run", "run_split", "run_packed", "run_split_packed")),
                        (att, ("run", "run_planned"))):
         for n in names:
             assert callable(getattr(obj, n))
@@ -62,10 +62,12 @@ def test_reference_call_sequence_matches_operator(dev, split):
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
     # the byte-union entry agrees with the packed bitmap
-    bytes_u = sel.run(gl, kcounts, qperm, qcounts, op.ns_t)
+    bytes_u = torch.empty(H, CQ, C, dtype=torch.uint8, device=dev)
+    rowcnt2 = torch.empty_like(rowcnt)
+    sel.run(gl, kcounts, qperm, qcounts, op.ns_t, bytes_u, rowcnt2)
     bits = ((unip.view(torch.uint8).unsqueeze(-1) >> torch.arange(8, device=dev, dtype=torch.uint8))
             & 1).reshape(H, CQ, C)
-    assert torch.equal(bytes_u.to(torch.uint8), bits)
+    assert torch.equal(bytes_u, bits) and torch.equal(rowcnt2, rowcnt)
     # a reuse call (rebuild=False) through the same small plan reproduces it
     out2 = torch.empty_like(q)
     att.run_planned(q, kp, vp, qcounts, kcounts, unip.view(torch.uint8).reshape(H, CQ, C // 8),
@@ -75,3 +77,7 @@ def test_reference_call_sequence_matches_operator(dev, split):
     torch.cuda.synchronize()
     assert torch.equal(out2, ref)
     assert torch.equal(vp2, vp) and torch.equal(sumv2, sumv) and torch.equal(lam2, lam)
+    sumv3, lam3 = torch.empty_like(sumv), torch.empty_like(lam)
+    kmm.run_vstats(vp2, kcounts, sumv3, lam3)
+    torch.cuda.synchronize()
+    assert torch.equal(sumv3, sumv) and torch.equal(lam3, lam)

@@ -55,6 +55,12 @@ class KmmExt:
                          "qperm": qperm, "kcounts": kcounts, "kperm": kperm, "V_sorted": vp,
                          "sumv": sumv, "lam": lam})
 
+    def run_vstats(self, vp, counts, sumv, lam):
+        H, N, _ = vp.shape
+        CK = counts.shape[1]
+        ws = self._ws.get(("vst", vp.device, H, N, CK), ops.vstats_ws_bytes(H, N, CK), vp.device)
+        ops.vstats(vp, counts, sumv, lam, ws=ws)
+
     def run_vstats_gather(self, v, kperm, counts, vp, sumv, lam):
         H, N, _ = v.shape
         CK = counts.shape[1]
@@ -72,8 +78,16 @@ class SelectUnionExt:
         H, N, _ = gl.shape
         return self._ws.get((gl.device, H, N, CQ), ops.select_ws_bytes(H, N, CQ), gl.device)
 
-    def run(self, gl, counts, qperm, tile_sizes, ns_t):
-        return ops.select_union_bytes(gl, counts, qperm, tile_sizes, ns_t)
+    def run(self, gl, counts, qperm, tile_sizes, ns_t, uni, rowcnt):
+        ops.select_union_bytes(gl, counts, qperm, tile_sizes, ns_t, uni=uni, rowcnt=rowcnt,
+                               ws=self._wsbuf(gl, tile_sizes.shape[1]))
+
+    def run_split(self, gl, counts, qperm, tile_sizes, split_cap, ns_t, uni, rowcnt,
+                  virtual_sizes, off, vbase, nsplit):
+        # the union does not depend on how rows are split across work-groups
+        if int(split_cap) < 1:
+            raise ValueError("t2t: split_cap must be >= 1")
+        self.run(gl, counts, qperm, tile_sizes, ns_t, uni, rowcnt)
 
     def run_packed(self, gl, counts, qperm, tile_sizes, ns_t, partial, unip, rowcnt, off):
         ops.select_union(gl, counts, qperm, tile_sizes, ns_t, unip=unip, rowcnt=rowcnt,

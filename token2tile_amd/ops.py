@@ -161,14 +161,19 @@ def select_union(gl, kcounts, qperm, qcounts, ns_t, unip=None, rowcnt=None, ws=N
     return unip, rowcnt
 
 
-def select_union_bytes(gl, kcounts, qperm, qcounts, ns_t, stream=None):
+def select_union_bytes(gl, kcounts, qperm, qcounts, ns_t, uni=None, rowcnt=None, ws=None,
+                       stream=None):
     """Byte-per-cluster union [H, CQ, 2048] uint8 (the reference's `run`)."""
     H, N, CK = gl.shape
     CQ = qcounts.shape[1]
     dev = _dev(gl)
-    uni = torch.empty(H, CQ, CK, dtype=torch.uint8, device=dev)
-    rowcnt = torch.empty(H, N, dtype=_i32, device=dev)
-    ws = _ws(select_ws_bytes(H, N, CQ), dev)
+    uni = torch.empty(H, CQ, CK, dtype=torch.uint8, device=dev) if uni is None else uni
+    rowcnt = torch.empty(H, N, dtype=_i32, device=dev) if rowcnt is None else rowcnt
+    _check(uni, (H, CQ, CK), torch.uint8, "uni")
+    _check(rowcnt, (H, N), _i32, "rowcnt")
+    need = select_ws_bytes(H, N, CQ)
+    if ws is None or ws.numel() < need:
+        ws = _ws(need, dev)
     call("t2t_select_run", gl, kcounts, qperm, qcounts, ns_t, uni, rowcnt, H, N, CQ, ws, ws.numel(),
          stream_handle(stream))
     return uni, rowcnt
