@@ -167,21 +167,31 @@ int t2t_tile_attn_exact(const void* q, const void* kp, const void* vp, int dtype
                         const int32_t* kcounts, const int32_t* unip, const int32_t* qperm,
                         const int32_t* plan, void* attn_out, float* lse,
                         int H, int N, int CQ, void* stream);
+/* Bytes of the centroid tile image (cks and transposed sumv in the layout
+ * the residual kernel stages into LDS), H x 32 tiles of 20480 bytes. */
+size_t t2t_centroid_tiles_bytes(int H);
+/* Workspace bytes of t2t_tail_merge (the centroid tile image). */
+size_t t2t_tail_merge_ws_bytes(int H);
 /* Centroid residual over the clusters outside each query's union and the
- * merge with the exact part under one softmax (S6); out in the ORIGINAL
- * order.  tailw_dev: 0-dim fp32 on device.
+ * merge with the exact part under one softmax (S6); attn_out and lse in the
+ * SORTED order, out in the ORIGINAL order.  tailw_dev: 0-dim fp32 on device.
+ * ws >= t2t_tail_merge_ws_bytes(H).
  * Replaces launch_tail_merge, tile_attn/src/kernel.cu:1478-1495. */
 int t2t_tail_merge(const void* attn_out, const float* lse, const void* QU,
                    const void* cks, const void* sumv, const int32_t* kcounts,
                    const int32_t* unip, const int32_t* qlab,
                    const int32_t* qperm, const float* lam, const float* tailw_dev,
-                   void* out, int dtype, int H, int N, int CQ, void* stream);
-/* attn_out/lse workspace bytes for t2t_tile_attn_run(_planned). */
+                   void* out, int dtype, int H, int N, int CQ,
+                   void* ws, size_t ws_bytes, void* stream);
+/* Workspace bytes of t2t_tile_attn_run_planned: lse [H, N] fp32 and the
+ * centroid tile image. */
 size_t t2t_tile_attn_ws_bytes(int H, int N, int dtype);
 /* Plan (when rebuild_plan != 0), exact attention, residual and merge in
- * one call.  Replaces tile_attn_ext.run_planned,
- * kernels/tile_attn/src/main.cpp:67-79; ws holds attn_out and lse (the
- * reference allocates them per call). */
+ * one call: the exact part is written to the original rows of out and the
+ * residual kernel merges into them in place.  Replaces
+ * tile_attn_ext.run_planned, kernels/tile_attn/src/main.cpp:67-79; ws holds
+ * lse and the centroid tiles (the reference allocates attn_out and lse per
+ * call). */
 int t2t_tile_attn_run_planned(const void* q, const void* kp, const void* vp, int dtype,
                               const int32_t* qcounts, const int32_t* kcounts,
                               const int32_t* unip, const void* QU, const void* cks,

@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(L, n), n
         assert n in _lib.SIGNATURES, f"{n} missing from the ctypes signature table"
     assert set(_lib.SIGNATURES) == set(names)
-    assert L.t2t_abi_version() == 100
+    assert L.t2t_abi_version() == 101
 
 
 def test_workspace_queries():

@@ -235,7 +235,7 @@ def attn_case(rng, H=2, N=3000, CQ=24, density=0.1, empty_cluster=True):
     qlab = rng.integers(0, CQ, (H, N)).astype(np.int32)
     if empty_cluster:
         qlab[qlab == 5] = 6
-    qlab[:, :300] = 7                                        # one large cluster (> 128 rows)
+    qlab[:, :600] = 7                                        # one large cluster (> 128 rows)
     qperm, qcounts = O.stable_perm(qlab, CQ)
     sel = rng.random((H, CQ, 2048)) < density
     sel[:, 3] = False                                        # an empty union

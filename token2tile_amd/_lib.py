@@ -45,8 +45,10 @@ SIGNATURES = {
     "t2t_tile_plan": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P]),
     "t2t_tile_attn_exact": (c_int, [_P, _P, _P, c_int, _P, _P, _P, _P, _P, _P, c_int, c_int,
                                     c_int, _P]),
+    "t2t_centroid_tiles_bytes": (c_size_t, [c_int]),
+    "t2t_tail_merge_ws_bytes": (c_size_t, [c_int]),
     "t2t_tail_merge": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int,
-                               c_int, c_int, _P]),
+                               c_int, c_int, _P, c_size_t, _P]),
     "t2t_tile_attn_ws_bytes": (c_size_t, [c_int, c_int, c_int]),
     "t2t_tile_attn_run_planned": (c_int, [_P, _P, _P, c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                           _P, _P, _P, c_int, c_int, c_int, c_int, _P, c_size_t,

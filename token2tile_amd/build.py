@@ -30,13 +30,17 @@ FLAGS = [
 ]
 
 
+# per-file extra compiler flags
+EXTRA: dict = {}
+
+
 def sources():
     return sorted(CSRC.glob("*.hip"))
 
 
 def _compile(src: Path, debug: bool) -> Path:
     obj = OBJ / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if debug:
         cmd += ["-g"]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -23,7 +23,7 @@ int t2t_check_launch(const char* what) {
 }
 
 extern "C" const char* t2t_last_error(void) { return g_err; }
-extern "C" int t2t_abi_version(void) { return 100; }
+extern "C" int t2t_abi_version(void) { return 101; }
 
 // ---------------------------------------------------------------------------
 // row gather: out[h, i] = x[h, perm[h, i]]  (16-byte vectors, 16 B per lane)

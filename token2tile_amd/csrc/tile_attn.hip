@@ -1,21 +1,23 @@
 // S5/S6: task planning, exact attention over each query cluster's union of
 // key clusters, and the centroid residual + merge (gfx950, MFMA 32x32x16).
 //
-// Exact attention (one work-group per task of <= 256 sorted queries of one
-// query cluster, 8 waves x 32 queries):
-//   * the union is turned into runs of cluster-ordered key rows in LDS;
-//   * 64-key tiles of K (row major) and V (transposed, key-contiguous) are
-//     gathered from kp/vp into a double-buffered LDS ring: tile t is consumed
-//     while tile t+1 is written from registers and tile t+2 is in flight, one
-//     barrier per tile;
+// Exact attention (one work-group per task of <= 128 sorted queries of one
+// query cluster, 4 waves x 32 queries, two work-groups per CU):
+//   * the union is turned into runs of cluster-ordered key rows in LDS, and
+//     the kp/vp rows of every 64-key tile are derived from them in parallel;
+//   * K and V tiles are gathered by LDS DMA into a double-buffered ring, row
+//     major with an XOR swizzle; tile t is consumed while tile t+1 is in
+//     flight, one barrier per tile;
+//   * S^T = K Q^T and O^T = V^T P^T on MFMA, so every lane owns one query: the
+//     online-softmax max/sum need one cross-half exchange, and the per-query
+//     rescale of O touches only the lane's own registers; V^T operands come
+//     from transposing LDS reads;
 //   * the running max advances with a margin, so O is rescaled only when a
-//     tile raises the max by more than the margin;
-//   * S^T = K Q^T and O^T = V^T P^T on MFMA, so every lane owns one query:
-//     the online-softmax max/sum need one cross-half exchange, and the
-//     per-query rescale of O touches only the lane's own registers.
-// Residual (one work-group per 128 sorted queries): the same structure over
-// the 2048 centroids (K = cks, V = sumv), masked by the query's union,
-// followed by the merge with the exact part.
+//     tile raises the max by more than the margin.
+// Residual + merge (a separate kernel, one work-group per 128 consecutive
+// sorted queries): the same structure over the 2048 centroids (K = cks,
+// V = sumv, staged from a per-call tile image), each lane masking its own
+// query cluster's union, then the merge with the exact part.
 #include "t2t_common.h"
 #include <type_traits>
 
@@ -24,7 +26,6 @@
 #define TA_QT 128   // queries per task (4 waves x 32)
 #define TA_WAVES 4
 #define TA_KT 64    // keys per tile
-#define TA_VP 68    // residual-only sVt pitch (halves) of the unfused tail kernel
 
 // ---------------------------------------------------------------------------
 // plan layout (int32): k_off [H][2049] | kvlen [H][CQ] | ntask [H] |
@@ -219,6 +220,8 @@ __device__ inline int xcd_remap(int bid, int total) {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
 // LDS tile layouts (no padding, XOR swizzles keep the MFMA operand reads
 // conflict free):
@@ -242,26 +245,31 @@ __device__ inline uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_am
 #define T2T_REAL_BRANCH() asm volatile("" ::: "memory")
 
 // One work-group (4 waves, 32 queries each) per task of <= 128 queries, two
-// work-groups per CU.  FUSE = false: exact attention only, attn_out and lse
-// (log2 units) in sorted order.  FUSE = true: exact attention, then the
-// residual over the centroids outside the task's (shared) union and the
-// merge under one softmax, written at the original rows.
-template <typename T, bool FUSE>
+// work-groups per CU.  MODE 0: attn_out and lse (log2 units) in sorted order.
+// MODE 1: the exact output at the original rows of out, lse in sorted order
+// (the residual kernel merges into out in place).
+template <typename T, int MODE>
 __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kp,
     const uint16_t* __restrict__ vp, const uint32_t* __restrict__ unip,
     const int32_t* __restrict__ qperm, const int32_t* __restrict__ kcounts,
     const int32_t* __restrict__ k_off, const int32_t* __restrict__ ntask,
     const int32_t* __restrict__ tasks, uint16_t* __restrict__ attn_out, float* __restrict__ lse,
-    const uint16_t* __restrict__ QU, const uint16_t* __restrict__ cks,
-    const uint16_t* __restrict__ sumv, const float* __restrict__ lam,
-    const float* __restrict__ tailw, uint16_t* __restrict__ out, int H, int N, int CQ, int maxT) {
-  __shared__ __attribute__((aligned(1024))) uint16_t sK[2][TA_KT * 128];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[2][TA_D * 64];
-  __shared__ uint16_t runCl[TA_CK];
-  __shared__ int runCum[TA_CK + 1];
+    uint16_t* __restrict__ out, int H, int N, int CQ, int maxT) {
+  // two separate arrays (not one [2][...] array): the K DMA into one buffer
+  // must not be taken as a possible writer of the other one, or every read of
+  // the tile in use would wait for the loads of the tile in flight
+  __shared__ __attribute__((aligned(1024))) uint16_t sK0[TA_KT * 128];
+  __shared__ __attribute__((aligned(1024))) uint16_t sK1[TA_KT * 128];
+  __shared__ __attribute__((aligned(1024))) uint16_t sV0[TA_KT * 128];
+  __shared__ __attribute__((aligned(1024))) uint16_t sV1[TA_KT * 128];
+  // runs of the union: first key position (cum) and first kp/vp row of each
+  // run, as 24-bit values (16-bit low part + 8-bit high part; N < 2^24), so
+  // the index builder reads only LDS
+  __shared__ uint16_t runCumLo[TA_CK + 1], runRowLo[TA_CK];
+  __shared__ uint8_t runCumHi[TA_CK + 1], runRowHi[TA_CK];
   __shared__ int sIdx[2][TA_KT];
-  __shared__ __attribute__((aligned(16))) float sCnt[2][TL_CT];
+  __shared__ int bMark[TA_KT];
   __shared__ int wsc[TA_WAVES], wsr[TA_WAVES];
   const int total = H * maxT;
   const int lin = xcd_remap(blockIdx.x, total);
@@ -306,40 +314,52 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     if (cnts[j] > 0) {
-      runCl[r] = (uint16_t)(8 * tid + j);
-      runCum[r] = p;
+      const int row0 = ko[8 * tid + j];
+      runCumLo[r] = (uint16_t)p;
+      runCumHi[r] = (uint8_t)(p >> 16);
+      runRowLo[r] = (uint16_t)row0;
+      runRowHi[r] = (uint8_t)(row0 >> 16);
       ++r;
       p += cnts[j];
     }
   }
-  if (tid == 0) runCum[nrun] = kvlen;
+  if (tid == 0) {
+    runCumLo[nrun] = (uint16_t)kvlen;
+    runCumHi[nrun] = (uint8_t)(kvlen >> 16);
+  }
+  auto run_cum = [&](int r) { return (int)runCumLo[r] | ((int)runCumHi[r] << 16); };
+  auto run_row = [&](int r) { return (int)runRowLo[r] | ((int)runRowHi[r] << 16); };
 
   const int qrow = wave * 32 + jl;  // query row inside the task
   const bool qok = qrow < qrows;
   const bool wave_active = wave * 32 < qrows;
   const size_t obase = (size_t)h * N + qs;  // sorted-order rows of the task
   const int orig = qperm[obase + (qok ? qrow : 0)];
-  const int kq = tid >> 4, dseg = tid & 15;  // V loader: 4 keys (4 kq ..) x 8 dims (dseg)
-
-  // ---- stage 4 rows x 8 dims into the transposed, swizzled sVt[buf]
-  auto stash_vt = [&](int buf, const u32x4 (&v)[4]) {
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const u32x2 lo = {pack_lo(v[0][w], v[1][w]), pack_lo(v[2][w], v[3][w])};
-      const u32x2 hi = {pack_hi(v[0][w], v[1][w]), pack_hi(v[2][w], v[3][w])};
-      *(u32x2*)(sVt[buf] + vt_gran_off(8 * dseg + 2 * w, kq)) = lo;
-      *(u32x2*)(sVt[buf] + vt_gran_off(8 * dseg + 2 * w + 1, kq)) = hi;
-    }
-  };
-  // ---- O^T += V^T P^T over one 64-key tile
-  auto pv = [&](f32x16 (&Oa)[4], int buf, const u32x4 (&pb)[4], auto mf) {
+  // ---- O^T += V^T P^T over one 64-key tile, V^T read from the row-major V
+  // tile by two transposing reads per operand.  In a 16-lane group, lane i of
+  // ds_read_b64_tr_b16 gets, in slot k, element i % 4 of the 8 bytes that lane
+  // 4 k + i / 4 addresses.  Lane l addresses key 16 mm + 8 r + 4 hh +
+  // (l % 16) / 4 at dims D + 4 (l % 4) .. + 3, D = 32 nb + 16 ((l / 16) % 2),
+  // and so receives dim D + l % 16 of keys 16 mm + 8 r + 4 hh + 0 .. 3: the
+  // operand elements t = 4 r + k, which hold keys 8 (t / 4) + 4 hh + t % 4 of
+  // the k-step, the order the P fragments are packed in.
+  const int trkey = 4 * hh + ((lane & 15) >> 2);
+  const int trdim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  auto pv = [&](f32x16 (&Oa)[4], const uint16_t* sVb, const u32x4 (&pb)[4]) {
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
-      const int dim = 32 * nb + jl;
 #pragma unroll
       for (int mm = 0; mm < 4; ++mm) {
-        const u32x4 a = *(const u32x4*)(sVt[buf] + vt_unit_off(dim, 2 * mm + hh));
-        Oa[nb] = mf(a, pb[mm], Oa[nb]);
+        u32x2 part[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int key = 16 * mm + 8 * r + trkey, dim = 32 * nb + trdim;
+          const uint16_t* src = sVb + key * 128 + 8 * ((dim >> 3) ^ (key & 15)) + (dim & 7);
+          part[r] = __builtin_bit_cast(
+              u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)src));
+        }
+        const u32x4 a = {part[0][0], part[0][1], part[1][0], part[1][1]};
+        Oa[nb] = Mfma<T>::run(a, pb[mm], Oa[nb]);
       }
     }
   };
@@ -365,49 +385,71 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
       for (int s = 0; s < 8; ++s) qb[s] = *(const u32x4*)(qr + 16 * s);
     }
     const char* kh = (const char*)(kp + (size_t)h * N * TA_D);
-    const char* vh = (const char*)(vp + (size_t)h * N * TA_D) + 16 * dseg;
+    const char* vh = (const char*)(vp + (size_t)h * N * TA_D);
     const int ntile = (kvlen + TA_KT - 1) / TA_KT;
-    int cur = 0;  // run cursor of the index builders (threads 0..63)
     // source rows of tile `tile` -> sIdx[tile & 1]; past the end -> row 0
-    // (its keys are masked and its values multiply a zero probability)
+    // (its keys are masked and its values multiply a zero probability).
+    // Built by the last wave (idle in tasks of <= 96 rows) without loops:
+    // every run is non-empty, so runs r0 .. r0 + 63 cover the tile, r0 being
+    // the run that holds its first position.  Lane j reads run r0 + j and
+    // marks the tile slot where that run starts; a prefix max over the marks
+    // gives each position its run.
+    int r0 = 0;
     auto build_idx = [&](int tile) {
-      if (tid < TA_KT) {
-        const int pos = tile * TA_KT + tid;
-        int row = 0;
-        if (pos < kvlen) {
-          while (runCum[cur + 1] <= pos) ++cur;
-          row = ko[runCl[cur]] + pos - runCum[cur];
+      if (wave == TA_WAVES - 1) {
+        const int base = tile * TA_KT;
+        const int r = r0 + lane;
+        int cs = 0x7fffffff, rw = 0;
+        if (r < nrun) {
+          cs = run_cum(r);
+          rw = run_row(r);
         }
-        sIdx[tile & 1][tid] = row;
+        const int st = cs - base;  // lane 0: <= 0; other valid lanes: > 0
+        bMark[lane] = 0;
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0 || st < TA_KT) bMark[lane == 0 ? 0 : st] = lane + 1;
+        __builtin_amdgcn_wave_barrier();
+        int k = bMark[lane] - 1;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const int y = __shfl_up(k, d, 64);
+          if (lane >= d) k = k > y ? k : y;
+        }
+        const int pos = base + lane;
+        const int ck = __shfl(cs, k, 64), rk = __shfl(rw, k, 64);
+        sIdx[tile & 1][lane] = pos < kvlen ? rk + pos - ck : 0;
+        // run holding the next tile's first position
+        r0 += __popcll(__ballot(st <= TA_KT)) - 1;
       }
     };
-    u32x4 ldv[4];
-    // K tile via LDS DMA (each wave instruction fills 4 whole rows, the lane
-    // fetching the chunk that belongs at its swizzled position), V tile into
-    // registers for the transposed store
-    auto issue = [&](int tile) {
-      const int buf = tile & 1;
+    // K and V tiles via LDS DMA (each wave instruction fills 4 whole rows, the
+    // lane fetching the 16-byte chunk that belongs at its swizzled position)
+    auto issue = [&](int tile, auto BUF) {
+      constexpr int buf = decltype(BUF)::value;
+      uint16_t* sKb = buf ? sK1 : sK0;
+      uint16_t* sVb = buf ? sV1 : sV0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int blk = 4 * i + wave;
         const int row = 4 * blk + (lane >> 4);
         const uint32_t off = (uint32_t)sIdx[buf][row] * 256u + 16u * ((lane & 15) ^ (row & 15));
         __builtin_amdgcn_global_load_lds((const glb_void_t*)(kh + off),
-                                         (lds_void_t*)(sK[buf] + blk * 4 * 128), 16, 0, 0);
+                                         (lds_void_t*)(sKb + blk * 4 * 128), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const glb_void_t*)(vh + off),
+                                         (lds_void_t*)(sVb + blk * 4 * 128), 16, 0, 0);
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        ldv[i] = *(const u32x4*)(vh + (uint32_t)sIdx[buf][4 * kq + i] * 256u);
     };
     // one 64-key tile of the online softmax; MASK: the last, partial tile
-    auto tile_step = [&](int buf, int valid, auto MASK) {
+    auto tile_step = [&](auto BUF, int valid, auto MASK) {
+      constexpr int buf = decltype(BUF)::value;
+      const uint16_t* sKb = buf ? sK1 : sK0;
       f32x16 S[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         S[kb] = zero16();
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-          const u32x4 a = *(const u32x4*)(sK[buf] + sk_off(32 * kb + jl, 2 * s + hh));
+          const u32x4 a = *(const u32x4*)(sKb + sk_off(32 * kb + jl, 2 * s + hh));
           S[kb] = Mfma<T>::run(a, qb[s], S[kb]);
         }
       }
@@ -446,35 +488,46 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
           lsum = Pk<T>::sum2(pk, lsum);
           pb[2 * kb + a / 8][(a % 8) / 2] = pk;
         }
-      pv(O, buf, pb, [](const u32x4& a_, const u32x4& b_, const f32x16& c_) {
-        return Mfma<T>::run(a_, b_, c_);
-      });
+      pv(O, buf ? sV1 : sV0, pb);
     };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
     __syncthreads();  // runs visible
     build_idx(0);
     if (ntile > 1) build_idx(1);
     __syncthreads();
-    issue(0);
-    stash_vt(0, ldv);
+    issue(0, B0{});
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (ntile > 1) issue(1);
+    if (ntile > 1) issue(1, B1{});
     if (ntile > 2) build_idx(2);
-    // full tiles in the loop; a partial last tile is peeled after it (one
-    // masked copy of the tile body outside the loop keeps register pressure
-    // of the loop at that of the unmasked body)
+    // one full tile held in buffer BUF: consume it, stage the V of the next
+    // tile, wait for the next tile's K, then start the tile after it
+    auto body = [&](int tile, auto BUF) {
+      constexpr int buf = decltype(BUF)::value;
+      if (wave_active) tile_step(BUF, TA_KT, std::false_type{});
+      __builtin_amdgcn_s_waitcnt(0);  // K and V DMA of tile + 1 landed
+      __syncthreads();
+      if (tile + 2 < ntile) issue(tile + 2, BUF);
+      if (tile + 3 < ntile) build_idx(tile + 3);
+    };
+    // full tiles two at a time, so that each buffer is a compile-time
+    // constant; a partial last tile is peeled after the loop (a masked copy of
+    // the tile body inside the loop would raise its register pressure)
     const int nfull = (kvlen % TA_KT) ? ntile - 1 : ntile;
     int tile = 0;
-    for (; tile < nfull; ++tile) {
-      const int buf = tile & 1;
-      if (wave_active) tile_step(buf, TA_KT, std::false_type{});
-      if (tile + 1 < ntile) stash_vt(buf ^ 1, ldv);
-      __builtin_amdgcn_s_waitcnt(0);  // K DMA of tile + 1 landed
-      __syncthreads();
-      if (tile + 2 < ntile) issue(tile + 2);
-      if (tile + 3 < ntile) build_idx(tile + 3);
+    for (; tile + 2 <= nfull; tile += 2) {
+      body(tile, B0{});
+      body(tile + 1, B1{});
     }
-    if (tile < ntile && wave_active) tile_step(tile & 1, kvlen - tile * TA_KT, std::true_type{});
+    if (tile < nfull) body(tile++, B0{});
+    if (tile < ntile && wave_active) {
+      const int valid = kvlen - tile * TA_KT;
+      if (tile & 1)
+        tile_step(B1{}, valid, std::true_type{});
+      else
+        tile_step(B0{}, valid, std::true_type{});
+    }
   }
   const float lt = lsum + __shfl_xor(lsum, 32, 64);
   const float inv = kvlen > 0 ? 1.0f / lt : 0.f;
@@ -483,7 +536,8 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
   // holds it: sorted-order attn_out (exact-only kernel) or, for the fused
   // kernel, the original row of out, read back by the merge
   if (qok) {
-    uint16_t* orow = FUSE ? out + ((size_t)h * N + orig) * TA_D : attn_out + (obase + qrow) * TA_D;
+    uint16_t* orow =
+        MODE != 0 ? out + ((size_t)h * N + orig) * TA_D : attn_out + (obase + qrow) * TA_D;
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
@@ -492,326 +546,226 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
             u32x2{Pk<T>::pack(O[nb][4 * g] * inv, O[nb][4 * g + 1] * inv),
                   Pk<T>::pack(O[nb][4 * g + 2] * inv, O[nb][4 * g + 3] * inv)};
   }
-  if constexpr (!FUSE) {
-    if (qok && hh == 0) lse[obase + qrow] = lse2;
-    return;
-  } else {
-    // ---------------- residual over the centroids outside the union ----------
-    // Centroids inside the union are staged with zero count and zero value
-    // sum, so they add nothing to phi or O and need no per-score test.
-    const float L2E = 1.4426950408889634f;
-    uint32_t todo = 0;  // centroid tiles not entirely inside the union
-#pragma unroll 1
-    for (int tc = 0; tc < TA_CK / TL_CT; ++tc)
-      if ((ur[2 * tc] & ur[2 * tc + 1]) != 0xffffffffu) todo |= 1u << tc;
-    u32x4 qu0, qu1;
-    {
-      const uint16_t* qr = QU + ((size_t)h * N + orig) * 32 + 8 * hh;
-      qu0 = *(const u32x4*)(qr);
-      qu1 = *(const u32x4*)(qr + 16);
-    }
-    const uint16_t* chh = cks + (size_t)h * TA_CK * 32;
-    const uint16_t* shh = sumv + (size_t)h * TA_CK * TA_D + 8 * dseg;
-    u32x4 lc, lv[4];
-    float lcnt = 0.f;
-    auto issue_r = [&](int tc) {
-      lc = *(const u32x4*)(chh + (size_t)(tc * TL_CT + (tid >> 2)) * 32 + 8 * (tid & 3));
-      const uint32_t w4 = (ur[2 * tc + (kq >> 3)] >> (4 * (kq & 7))) & 0xfu;  // my 4 centroids
+  if (qok && hh == 0) lse[obase + qrow] = lse2;
+}
+
+template <typename T, int MODE>
+static void launch_attn(const void* q, const void* kp, const void* vp, const int32_t* unip,
+                        const int32_t* qperm, const int32_t* kcounts, const PlanView& p,
+                        void* attn_out, float* lse, void* out, int H, int N, int CQ,
+                        hipStream_t st) {
+  const int total = H * p.maxT;
+  const int grid = ((total + 7) / 8) * 8;
+  hipLaunchKernelGGL((attn_kernel<T, MODE>), dim3(grid), dim3(TA_WAVES * 64), 0, st,
+                     (const uint16_t*)q, (const uint16_t*)kp, (const uint16_t*)vp,
+                     (const uint32_t*)unip, qperm, kcounts, p.k_off, p.ntask, p.tasks,
+                     (uint16_t*)attn_out, lse, (uint16_t*)out, H, N, CQ, p.maxT);
+}
+
+// ---------------------------------------------------------------------------
+// residual over the centroids outside each query's union + merge
+// ---------------------------------------------------------------------------
+// Centroid tile image, built once per call and staged by LDS DMA: per head,
+// 32 tiles of 64 centroids, RT_BYTES each:
+//   [0, 4096)      cks rows, 64 x 32 halves; 16-byte chunk c of row r sits at
+//                  chunk c ^ ((r >> 2) & 3), so the MFMA operand reads of 16
+//                  consecutive rows hit distinct banks
+//   [4096, 20480)  sumv transposed, 128 dims x 64 centroids in the sVt layout
+#define RT_TILES (TA_CK / TL_CT)
+#define RT_BYTES 20480
+#define RT_HALVES (RT_BYTES / 2)
+__device__ inline int rc_off(int r, int c) { return r * 32 + 8 * (c ^ ((r >> 2) & 3)); }
+
+__global__ __launch_bounds__(256) void centroid_tiles_kernel(const uint16_t* __restrict__ cks,
+                                                             const uint16_t* __restrict__ sumv,
+                                                             uint16_t* __restrict__ tiles) {
+  const int tc = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  uint16_t* dst = tiles + ((size_t)h * RT_TILES + tc) * RT_HALVES;
+  const uint16_t* ch = cks + ((size_t)h * TA_CK + tc * TL_CT) * 32;
+  const uint16_t* vh = sumv + ((size_t)h * TA_CK + tc * TL_CT) * TA_D;
+  {
+    const int r = tid >> 2, c = tid & 3;
+    *(u32x4*)(dst + rc_off(r, c)) = *(const u32x4*)(ch + r * 32 + 8 * c);
+  }
+  // thread: 4 centroids (kq) x 8 dims (dseg), transposed into 4-centroid granules
+  const int kq = tid >> 4, dseg = tid & 15;
+  u32x4 v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        lv[i] = *(const u32x4*)(shh + (size_t)(tc * TL_CT + 4 * kq + i) * TA_D);
-        if ((w4 >> i) & 1u) lv[i] = u32x4{0u, 0u, 0u, 0u};
-      }
-      if (tid < TL_CT)
-        lcnt = ((ur[2 * tc + (tid >> 5)] >> (tid & 31)) & 1u) ? 0.f : (float)kc[tc * TL_CT + tid];
-    };
-    auto stash_r = [&](int buf) {
-      *(u32x4*)(sK[buf] + (tid >> 2) * TL_CP + 8 * (tid & 3)) = lc;
-      stash_vt(buf, lv);
-      if (tid < TL_CT) sCnt[buf][tid] = lcnt;
-    };
-    float m2 = -__builtin_inff(), phi = 0.f;
+  for (int i = 0; i < 4; ++i) v[i] = *(const u32x4*)(vh + (size_t)(4 * kq + i) * TA_D + 8 * dseg);
+  uint16_t* vt = dst + 2048;
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) O[nb] = zero16();
-    __syncthreads();  // the exact loop's buffers are free
-    uint32_t rest = todo;
-    int tcur = rest ? __builtin_ctz(rest) : -1;
-    if (rest) rest &= rest - 1;
-    int tnext = rest ? __builtin_ctz(rest) : -1;
-    if (rest) rest &= rest - 1;
-    if (tcur >= 0) {
-      issue_r(tcur);
-      stash_r(0);
-      if (tnext >= 0) issue_r(tnext);
-    }
-    __syncthreads();
-    int buf = 0;
-    while (tcur >= 0) {
-      // scores of the lane's query against 32 kb + 8 (a / 4) + 4 hh + a % 4,
-      // rounded to fp16 as the selection's scores are
-      uint32_t sh[2][8];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const uint16_t* crow = sK[buf] + (32 * kb + jl) * TL_CP + 8 * hh;
-        f32x16 S = zero16();
-        S = Mfma<F16T>::run(*(const u32x4*)(crow), qu0, S);
-        S = Mfma<F16T>::run(*(const u32x4*)(crow + 16), qu1, S);
-#pragma unroll
-        for (int a = 0; a < 16; a += 2) sh[kb][a / 2] = Pk<F16T>::pack(S[a], S[a + 1]);
-      }
-      float sv[2][16];
-      float mx = -__builtin_inff();
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int a = 0; a < 16; a += 2) {
-          sv[kb][a] = h2f((uint16_t)(sh[kb][a / 2] & 0xffffu));
-          sv[kb][a + 1] = h2f((uint16_t)(sh[kb][a / 2] >> 16));
-          mx = vmax(mx, vmax(sv[kb][a], sv[kb][a + 1]));
-        }
-      mx = vmax(mx, __shfl_xor(mx, 32, 64));
-      if (__builtin_amdgcn_readfirstlane((int)(__ballot(mx > m2) != 0ull))) {
-        T2T_REAL_BRANCH();
-        const float mnew = mx > m2 ? mx + TL_MARGIN : m2;
-        const float alpha = __builtin_amdgcn_exp2f((m2 - mnew) * L2E);
-        m2 = mnew;
-        phi *= alpha;
-        rescale(O, alpha);
-      }
-      const float nm = -m2 * L2E;
-      u32x4 pb[4];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          // counts of centroids 32 kb + 8 j + 4 hh .. + 3
-          const f32x4 cn = *(const f32x4*)(sCnt[buf] + 32 * kb + 8 * j + 4 * hh);
-          float pe[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            pe[e] = __builtin_amdgcn_exp2f(fmaf(sv[kb][4 * j + e], L2E, nm));
-            phi = fmaf(pe[e], cn[e], phi);
-          }
-          pb[2 * kb + j / 2][2 * (j % 2)] = Pk<F16T>::pack(pe[0], pe[1]);
-          pb[2 * kb + j / 2][2 * (j % 2) + 1] = Pk<F16T>::pack(pe[2], pe[3]);
-        }
-      pv(O, buf, pb, [](const u32x4& a_, const u32x4& b_, const f32x16& c_) {
-        return Mfma<F16T>::run(a_, b_, c_);
-      });
-      if (tnext >= 0) stash_r(buf ^ 1);
-      const int tn2 = rest ? __builtin_ctz(rest) : -1;
-      if (rest) rest &= rest - 1;
-      __syncthreads();
-      if (tn2 >= 0) issue_r(tn2);
-      tcur = tnext;
-      tnext = tn2;
-      buf ^= 1;
-    }
-    if (!qok) return;
-    // ---------------- merge under one softmax --------------------------------
-    phi += __shfl_xor(phi, 32, 64);
-    const float tw = *tailw;
-    const float lm = lam[h];
-    const float le = lse2 * 0.6931471805599453f;
-    float ex, st;
-    if (le >= m2) {
-      ex = 1.0f;
-      st = __expf(m2 - le);
-    } else {
-      ex = __expf(le - m2);
-      st = 1.0f;
-    }
-    const float ph = st * phi;
-    const bool bad = ph <= 1.0e-6f * ex;
-    const float den = fmaxf(ex + ph * tw, 1.0e-12f);
-    const float wx = ex / den, wt = st * tw * lm / den;
-    if (bad) return;  // the exact part already written is the output
-    uint16_t* orow = out + ((size_t)h * N + orig) * TA_D;
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        u32x2 v = *(const u32x2*)(orow + 32 * nb + 8 * g + 4 * hh);  // exact part
-        const uint32_t w0 = v[0], w1 = v[1];
-        const float x0 = T::to_f((uint16_t)(w0 & 0xffff)), x1 = T::to_f((uint16_t)(w0 >> 16));
-        const float x2 = T::to_f((uint16_t)(w1 & 0xffff)), x3 = T::to_f((uint16_t)(w1 >> 16));
-        v[0] = Pk<T>::pack(fmaf(wt, O[nb][4 * g], wx * x0), fmaf(wt, O[nb][4 * g + 1], wx * x1));
-        v[1] = Pk<T>::pack(fmaf(wt, O[nb][4 * g + 2], wx * x2), fmaf(wt, O[nb][4 * g + 3], wx * x3));
-        *(u32x2*)(orow + 32 * nb + 8 * g + 4 * hh) = v;
-      }
+  for (int w = 0; w < 4; ++w) {
+    const u32x2 lo = {pack_lo(v[0][w], v[1][w]), pack_lo(v[2][w], v[3][w])};
+    const u32x2 hi = {pack_hi(v[0][w], v[1][w]), pack_hi(v[2][w], v[3][w])};
+    *(u32x2*)(vt + vt_gran_off(8 * dseg + 2 * w, kq)) = lo;
+    *(u32x2*)(vt + vt_gran_off(8 * dseg + 2 * w + 1, kq)) = hi;
   }
 }
 
-template <typename T, bool FUSE>
-static void launch_attn(const void* q, const void* kp, const void* vp, const int32_t* unip,
-                        const int32_t* qperm, const int32_t* kcounts, const PlanView& p,
-                        void* attn_out, float* lse, const void* QU, const void* cks,
-                        const void* sumv, const float* lam, const float* tailw, void* out, int H,
-                        int N, int CQ, hipStream_t st) {
-  const int total = H * p.maxT;
-  const int grid = ((total + 7) / 8) * 8;
-  hipLaunchKernelGGL((attn_kernel<T, FUSE>), dim3(grid), dim3(TA_WAVES * 64), 0, st,
-                     (const uint16_t*)q, (const uint16_t*)kp, (const uint16_t*)vp,
-                     (const uint32_t*)unip, qperm, kcounts, p.k_off, p.ntask, p.tasks,
-                     (uint16_t*)attn_out, lse, (const uint16_t*)QU, (const uint16_t*)cks,
-                     (const uint16_t*)sumv, lam, tailw, (uint16_t*)out, H, N, CQ, p.maxT);
-}
-
-// ---------------------------------------------------------------------------
-// residual over unselected centroids + merge
-// ---------------------------------------------------------------------------
-#define TL_CT 64
-#define TL_CP 40  // cks tile pitch (halves)
-
-template <typename T>
-__global__ __launch_bounds__(256) void tail_kernel(
-    const uint16_t* __restrict__ attn_out, const float* __restrict__ attn_lse,
-    const uint16_t* __restrict__ QU, const uint16_t* __restrict__ cks,
-    const uint16_t* __restrict__ sumv, const int32_t* __restrict__ kcounts,
-    const uint32_t* __restrict__ unip, const int32_t* __restrict__ qlab,
-    const int32_t* __restrict__ qperm, const float* __restrict__ lam,
-    const float* __restrict__ tailw, uint16_t* __restrict__ out, int N, int CQ) {
-  __shared__ __attribute__((aligned(16))) uint16_t sC[TL_CT * TL_CP];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[TA_D * TA_VP];
-  __shared__ float sCnt[TL_CT];
+// One work-group per 128 consecutive sorted queries (4 waves x 32, queries of
+// several query clusters side by side): every lane masks the centroids of
+// its own cluster's union, so all waves carry real rows.  The exact part is
+// read from attn_out (sorted order, SRC_SORTED) or from the original rows of
+// out, and the merged result is written to the original rows of out.
+template <typename T, bool SRC_SORTED>
+__global__ __launch_bounds__(256, 2) void resid_kernel(
+    const uint16_t* __restrict__ exact, const float* __restrict__ lse2v,
+    const uint16_t* __restrict__ QU, const uint16_t* __restrict__ tiles,
+    const int32_t* __restrict__ kcounts, const uint32_t* __restrict__ unip,
+    const int32_t* __restrict__ qlab, const int32_t* __restrict__ qperm,
+    const float* __restrict__ lam, const float* __restrict__ tailw, uint16_t* __restrict__ out,
+    int N, int CQ) {
+  __shared__ __attribute__((aligned(1024))) uint16_t sT0[RT_HALVES];
+  __shared__ __attribute__((aligned(1024))) uint16_t sT1[RT_HALVES];
+  __shared__ __attribute__((aligned(16))) float sCnt[TA_CK];
   const int h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int jl = lane & 31, hh = lane >> 5;
-  const int j = blockIdx.x * 128 + wave * 32 + jl;  // sorted query position
-  const bool ok = j < N;
-  const int orig = qperm[(size_t)h * N + (ok ? j : 0)];
+  const int row = blockIdx.x * 128 + wave * 32 + jl;  // sorted position
+  const bool ok = row < N;
+  const int orig = qperm[(size_t)h * N + (ok ? row : 0)];
   const uint32_t* ur = unip + ((size_t)h * CQ + qlab[(size_t)h * N + orig]) * (TA_CK / 32);
-  u32x4 qb0, qb1;
+  u32x4 qu0, qu1;
   {
     const uint16_t* qr = QU + ((size_t)h * N + orig) * 32 + 8 * hh;
-    qb0 = *(const u32x4*)(qr);
-    qb1 = *(const u32x4*)(qr + 16);
+    qu0 = *(const u32x4*)(qr);
+    qu1 = *(const u32x4*)(qr + 16);
   }
-  const uint16_t* ch = cks + (size_t)h * TA_CK * 32;
-  const uint16_t* vh = sumv + (size_t)h * TA_CK * TA_D;
-  const int kq = tid >> 4, dseg = tid & 15;
+  const char* th = (const char*)(tiles + (size_t)h * RT_TILES * RT_HALVES) + wave * 1024 + lane * 16;
+  auto issue = [&](int tc, auto BUF) {
+    uint16_t* sb = decltype(BUF)::value ? sT1 : sT0;
+#pragma unroll
+    for (int i = 0; i < RT_BYTES / 4096; ++i)
+      __builtin_amdgcn_global_load_lds((const glb_void_t*)(th + (size_t)tc * RT_BYTES + i * 4096),
+                                       (lds_void_t*)((char*)sb + i * 4096 + wave * 1024), 16, 0, 0);
+  };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  issue(0, B0{});
+#pragma unroll
+  for (int i = 0; i < TA_CK / 256; ++i)
+    sCnt[tid + 256 * i] = (float)kcounts[(size_t)h * TA_CK + tid + 256 * i];
+  uint32_t uw0 = ur[0], uw1 = ur[1];
   const float L2E = 1.4426950408889634f;
-  float m = -__builtin_inff(), phi = 0.f;
+  float m2 = -1.0e30f, phi = 0.f;
   f32x16 O[4];
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) O[nb] = zero16();
-  for (int tc = 0; tc < TA_CK / TL_CT; ++tc) {
-    __syncthreads();
-    {  // cks tile: 64 x 32 halves = 256 x 16 B
-      const int cr = tid >> 2, cc = tid & 3;
-      *(u32x4*)(sC + cr * TL_CP + 8 * cc) =
-          *(const u32x4*)(ch + (size_t)(tc * TL_CT + cr) * 32 + 8 * cc);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  auto body = [&](int tc, auto BUF) {
+    constexpr int buf = decltype(BUF)::value;
+    const uint16_t* sb = buf ? sT1 : sT0;
+    if (tc + 1 < RT_TILES) issue(tc + 1, std::integral_constant<int, buf ^ 1>{});
+    uint32_t nw0 = 0, nw1 = 0;
+    if (tc + 1 < RT_TILES) {
+      nw0 = ur[2 * tc + 2];
+      nw1 = ur[2 * tc + 3];
     }
-    {  // sumv tile transposed: thread = 4 centroids x 8 dims
-      u32x4 v[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        v[i] = *(const u32x4*)(vh + (size_t)(tc * TL_CT + 4 * kq + i) * TA_D + 8 * dseg);
-#pragma unroll
-      for (int d = 0; d < 8; ++d) {
-        const int w = d >> 1, sh = (d & 1) * 16;
-        u32x2 o;
-        o[0] = ((v[0][w] >> sh) & 0xffffu) | (((v[1][w] >> sh) & 0xffffu) << 16);
-        o[1] = ((v[2][w] >> sh) & 0xffffu) | (((v[3][w] >> sh) & 0xffffu) << 16);
-        *(u32x2*)(sVt + (8 * dseg + d) * TA_VP + 4 * kq) = o;
-      }
-    }
-    if (tid < TL_CT) sCnt[tid] = (float)kcounts[(size_t)h * TA_CK + tc * TL_CT + tid];
-    __syncthreads();
-    f32x16 S[2];
+    // fp16 scores of the lane's query against centroids 32 kb + 8 (a / 4) +
+    // 4 hh + a % 4 of the tile; centroids in the query's union -> -inf
+    float sv[2][16];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const uint16_t* cr = sC + (32 * kb + jl) * TL_CP + 8 * hh;
-      S[kb] = zero16();
-      S[kb] = Mfma<F16T>::run(*(const u32x4*)(cr), qb0, S[kb]);
-      S[kb] = Mfma<F16T>::run(*(const u32x4*)(cr + 16), qb1, S[kb]);
+      const int r = 32 * kb + jl;
+      f32x16 S = zero16();
+      S = Mfma<F16T>::run(*(const u32x4*)(sb + rc_off(r, hh)), qu0, S);
+      S = Mfma<F16T>::run(*(const u32x4*)(sb + rc_off(r, 2 + hh)), qu1, S);
+      const uint32_t uw = kb ? uw1 : uw0;
+#pragma unroll
+      for (int a = 0; a < 16; a += 2) {
+        const uint32_t pk = Pk<F16T>::pack(S[a], S[a + 1]);
+        const int b0 = 8 * (a / 4) + 4 * hh + (a % 4);
+        sv[kb][a] = ((uw >> b0) & 1u) ? -__builtin_inff() : h2f((uint16_t)(pk & 0xffffu));
+        sv[kb][a + 1] = ((uw >> (b0 + 1)) & 1u) ? -__builtin_inff() : h2f((uint16_t)(pk >> 16));
+      }
     }
     float mx = -__builtin_inff();
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int a = 0; a < 16; ++a) {
-        S[kb][a] = h2f(f2h(S[kb][a]));  // scores are fp16, as in selection
-        mx = fmaxf(mx, S[kb][a]);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(m, mx);
-    const float alpha = __builtin_amdgcn_exp2f((m - mnew) * L2E);
-    m = mnew;
-    const uint32_t uw0 = ur[2 * tc], uw1 = ur[2 * tc + 1];
-    float ps = 0.f;
-    u32x4 pb[4];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const uint32_t uw = kb ? uw1 : uw0;
-#pragma unroll
-      for (int a = 0; a < 16; a += 2) {
-        const int b0 = 8 * (a / 4) + 4 * hh + (a % 4);
-        const bool in0 = (uw >> b0) & 1u, in1 = (uw >> (b0 + 1)) & 1u;
-        const float p0 = in0 ? 0.f : __builtin_amdgcn_exp2f((S[kb][a] - mnew) * L2E);
-        const float p1 = in1 ? 0.f : __builtin_amdgcn_exp2f((S[kb][a + 1] - mnew) * L2E);
-        ps = fmaf(p0, sCnt[32 * kb + b0], ps);
-        ps = fmaf(p1, sCnt[32 * kb + b0 + 1], ps);
-        pb[2 * kb + a / 8][(a % 8) / 2] = pack2(f2h(p0), f2h(p1));
-      }
-    }
-    phi = phi * alpha + ps;
-    if (alpha != 1.0f) {
+      for (int a = 0; a < 16; a += 2) mx = vmax(mx, vmax(sv[kb][a], sv[kb][a + 1]));
+    mx = vmax(mx, __shfl_xor(mx, 32, 64));
+    if (__builtin_amdgcn_readfirstlane((int)(__ballot(mx > m2) != 0ull))) {
+      T2T_REAL_BRANCH();
+      const float mnew = mx > m2 ? mx + TL_MARGIN : m2;
+      const float alpha = __builtin_amdgcn_exp2f((m2 - mnew) * L2E);
+      m2 = mnew;
+      phi *= alpha;
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
         for (int a = 0; a < 16; ++a) O[nb][a] *= alpha;
     }
+    const float nm = -m2 * L2E;
+    u32x4 pb[4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 cn = *(const f32x4*)(sCnt + TL_CT * tc + 32 * kb + 8 * j + 4 * hh);
+        float pe[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pe[e] = __builtin_amdgcn_exp2f(fmaf(sv[kb][4 * j + e], L2E, nm));
+          phi = fmaf(pe[e], cn[e], phi);
+        }
+        pb[2 * kb + j / 2][2 * (j % 2)] = Pk<F16T>::pack(pe[0], pe[1]);
+        pb[2 * kb + j / 2][2 * (j % 2) + 1] = Pk<F16T>::pack(pe[2], pe[3]);
+      }
+    const uint16_t* vt = sb + 2048;
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
-      const uint16_t* vr = sVt + (32 * nb + jl) * TA_VP + 4 * hh;
+      const int dim = 32 * nb + jl;
 #pragma unroll
-      for (int mm = 0; mm < 4; ++mm) {
-        const u32x2 lo = *(const u32x2*)(vr + 16 * mm);
-        const u32x2 hi = *(const u32x2*)(vr + 16 * mm + 8);
-        const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-        O[nb] = Mfma<F16T>::run(a, pb[mm], O[nb]);
-      }
+      for (int mm = 0; mm < 4; ++mm)
+        O[nb] = Mfma<F16T>::run(*(const u32x4*)(vt + vt_unit_off(dim, 2 * mm + hh)), pb[mm], O[nb]);
     }
+    uw0 = nw0;
+    uw1 = nw1;
+    __builtin_amdgcn_s_waitcnt(0);  // tile tc + 1 landed
+    __syncthreads();
+  };
+  for (int tc = 0; tc < RT_TILES; tc += 2) {
+    body(tc, B0{});
+    body(tc + 1, B1{});
   }
   if (!ok) return;
+  // ---- merge under one softmax
   phi += __shfl_xor(phi, 32, 64);
   const float tw = *tailw;
   const float lm = lam[h];
-  const float le = attn_lse[(size_t)h * N + j] * 0.6931471805599453f;
+  const float le = lse2v[(size_t)h * N + row] * 0.6931471805599453f;
   float ex, st;
-  if (le >= m) {
+  if (le >= m2) {
     ex = 1.0f;
-    st = __expf(m - le);
+    st = __expf(m2 - le);
   } else {
-    ex = __expf(le - m);
+    ex = __expf(le - m2);
     st = 1.0f;
   }
   const float ph = st * phi;
   const bool bad = ph <= 1.0e-6f * ex;
   const float den = fmaxf(ex + ph * tw, 1.0e-12f);
   const float wx = ex / den, wt = st * tw * lm / den;
-  const uint16_t* ar = attn_out + ((size_t)h * N + j) * TA_D;
+  const uint16_t* er = SRC_SORTED ? exact + ((size_t)h * N + row) * TA_D
+                                  : out + ((size_t)h * N + orig) * TA_D;
   uint16_t* orow = out + ((size_t)h * N + orig) * TA_D;
+  if (bad && !SRC_SORTED) return;  // the exact part in out is the output
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d0 = 32 * nb + 8 * g + 4 * hh;
-      const u32x2 av = *(const u32x2*)(ar + d0);
-      u32x2 ov = av;
+      u32x2 v = *(const u32x2*)(er + d0);
       if (!bad) {
-        float x[4];
-        x[0] = T::to_f((uint16_t)(av[0] & 0xffff));
-        x[1] = T::to_f((uint16_t)(av[0] >> 16));
-        x[2] = T::to_f((uint16_t)(av[1] & 0xffff));
-        x[3] = T::to_f((uint16_t)(av[1] >> 16));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = fmaf(wt, O[nb][4 * g + e], wx * x[e]);
-        ov[0] = pack2(T::from_f(x[0]), T::from_f(x[1]));
-        ov[1] = pack2(T::from_f(x[2]), T::from_f(x[3]));
+        const float x0 = T::to_f((uint16_t)(v[0] & 0xffff)), x1 = T::to_f((uint16_t)(v[0] >> 16));
+        const float x2 = T::to_f((uint16_t)(v[1] & 0xffff)), x3 = T::to_f((uint16_t)(v[1] >> 16));
+        v[0] = Pk<T>::pack(fmaf(wt, O[nb][4 * g], wx * x0), fmaf(wt, O[nb][4 * g + 1], wx * x1));
+        v[1] = Pk<T>::pack(fmaf(wt, O[nb][4 * g + 2], wx * x2), fmaf(wt, O[nb][4 * g + 3], wx * x3));
       }
-      *(u32x2*)(orow + d0) = ov;
+      *(u32x2*)(orow + d0) = v;
     }
 }
 
@@ -827,48 +781,71 @@ extern "C" int t2t_tile_attn_exact(const void* q, const void* kp, const void* vp
   T2T_REQUIRE(q && kp && vp && kcounts && unip && qperm && plan && attn_out && lse,
               "tile_attn_exact: null pointer");
   T2T_REQUIRE(check_dtype(dtype), "tile_attn_exact: dtype %d", dtype);
-  T2T_REQUIRE(H > 0 && N > 0 && CQ > 0, "tile_attn_exact: H=%d N=%d CQ=%d", H, N, CQ);
+  T2T_REQUIRE(H > 0 && N > 0 && N < (1 << 24) && CQ > 0, "tile_attn_exact: H=%d N=%d CQ=%d", H, N, CQ);
   PlanView p = plan_view((int32_t*)plan, H, N, CQ);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == T2T_F16)
-    launch_attn<F16T, false>(q, kp, vp, unip, qperm, kcounts, p, attn_out, lse, nullptr, nullptr,
-                             nullptr, nullptr, nullptr, nullptr, H, N, CQ, st);
+    launch_attn<F16T, 0>(q, kp, vp, unip, qperm, kcounts, p, attn_out, lse, nullptr, H, N, CQ, st);
   else
-    launch_attn<BF16T, false>(q, kp, vp, unip, qperm, kcounts, p, attn_out, lse, nullptr, nullptr,
-                              nullptr, nullptr, nullptr, nullptr, H, N, CQ, st);
+    launch_attn<BF16T, 0>(q, kp, vp, unip, qperm, kcounts, p, attn_out, lse, nullptr, H, N, CQ, st);
   T2T_LAUNCH_CHECK("tile_attn_exact");
   return T2T_OK;
 }
+
+extern "C" size_t t2t_centroid_tiles_bytes(int H) { return (size_t)H * RT_TILES * RT_BYTES; }
+
+static void launch_centroid_tiles(const void* cks, const void* sumv, void* tiles, int H,
+                                  hipStream_t st) {
+  hipLaunchKernelGGL(centroid_tiles_kernel, dim3(RT_TILES, H), dim3(256), 0, st,
+                     (const uint16_t*)cks, (const uint16_t*)sumv, (uint16_t*)tiles);
+}
+
+template <bool SRC_SORTED>
+static void launch_resid(int dtype, const void* exact, const float* lse, const void* QU,
+                         const void* tiles, const int32_t* kcounts, const int32_t* unip,
+                         const int32_t* qlab, const int32_t* qperm, const float* lam,
+                         const float* tailw, void* out, int H, int N, int CQ, hipStream_t st) {
+  const dim3 grid(cdiv(N, 128), H);
+  if (dtype == T2T_F16)
+    hipLaunchKernelGGL((resid_kernel<F16T, SRC_SORTED>), grid, dim3(256), 0, st,
+                       (const uint16_t*)exact, lse, (const uint16_t*)QU, (const uint16_t*)tiles,
+                       kcounts, (const uint32_t*)unip, qlab, qperm, lam, tailw, (uint16_t*)out, N,
+                       CQ);
+  else
+    hipLaunchKernelGGL((resid_kernel<BF16T, SRC_SORTED>), grid, dim3(256), 0, st,
+                       (const uint16_t*)exact, lse, (const uint16_t*)QU, (const uint16_t*)tiles,
+                       kcounts, (const uint32_t*)unip, qlab, qperm, lam, tailw, (uint16_t*)out, N,
+                       CQ);
+}
+
+extern "C" size_t t2t_tail_merge_ws_bytes(int H) { return t2t_centroid_tiles_bytes(H); }
 
 extern "C" int t2t_tail_merge(const void* attn_out, const float* lse, const void* QU,
                               const void* cks, const void* sumv, const int32_t* kcounts,
                               const int32_t* unip, const int32_t* qlab, const int32_t* qperm,
                               const float* lam, const float* tailw_dev, void* out, int dtype, int H,
-                              int N, int CQ, void* stream) {
+                              int N, int CQ, void* ws, size_t ws_bytes, void* stream) {
   T2T_REQUIRE(attn_out && lse && QU && cks && sumv && kcounts && unip && qlab && qperm && lam &&
                   tailw_dev && out,
               "tail_merge: null pointer");
   T2T_REQUIRE(check_dtype(dtype), "tail_merge: dtype %d", dtype);
   T2T_REQUIRE(H > 0 && N > 0 && CQ > 0, "tail_merge: H=%d N=%d CQ=%d", H, N, CQ);
-  const dim3 grid(cdiv(N, 128), H);
+  if (!ws || ws_bytes < t2t_tail_merge_ws_bytes(H)) {
+    t2t_set_error("tail_merge: workspace of %zu bytes, need %zu", ws_bytes,
+                  t2t_tail_merge_ws_bytes(H));
+    return T2T_ERR_WORKSPACE;
+  }
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == T2T_F16)
-    hipLaunchKernelGGL(tail_kernel<F16T>, grid, dim3(256), 0, st, (const uint16_t*)attn_out, lse,
-                       (const uint16_t*)QU, (const uint16_t*)cks, (const uint16_t*)sumv, kcounts,
-                       (const uint32_t*)unip, qlab, qperm, lam, tailw_dev, (uint16_t*)out, N, CQ);
-  else
-    hipLaunchKernelGGL(tail_kernel<BF16T>, grid, dim3(256), 0, st, (const uint16_t*)attn_out, lse,
-                       (const uint16_t*)QU, (const uint16_t*)cks, (const uint16_t*)sumv, kcounts,
-                       (const uint32_t*)unip, qlab, qperm, lam, tailw_dev, (uint16_t*)out, N, CQ);
+  launch_centroid_tiles(cks, sumv, ws, H, st);
+  launch_resid<true>(dtype, attn_out, lse, QU, ws, kcounts, unip, qlab, qperm, lam, tailw_dev, out,
+                     H, N, CQ, st);
   T2T_LAUNCH_CHECK("tail_merge");
   return T2T_OK;
 }
 
 extern "C" size_t t2t_tile_attn_ws_bytes(int H, int N, int dtype) {
-  (void)H;
-  (void)N;
   (void)dtype;
-  return 0;  // the fused kernel keeps the exact part in registers
+  return t2t_align256((size_t)H * N * sizeof(float)) + t2t_centroid_tiles_bytes(H);
 }
 
 extern "C" int t2t_tile_attn_run_planned(const void* q, const void* kp, const void* vp, int dtype,
@@ -878,25 +855,31 @@ extern "C" int t2t_tile_attn_run_planned(const void* q, const void* kp, const vo
                                          const int32_t* qperm, const float* tailw_dev, void* out,
                                          int32_t* plan, int rebuild_plan, int H, int N, int CQ,
                                          void* ws, size_t ws_bytes, void* stream) {
-  (void)ws;
-  (void)ws_bytes;
   T2T_REQUIRE(q && kp && vp && qcounts && kcounts && unip && QU && cks && sumv && lam && qlab &&
                   qperm && tailw_dev && out && plan,
               "tile_attn_run_planned: null pointer");
   T2T_REQUIRE(check_dtype(dtype), "tile_attn_run_planned: dtype %d", dtype);
-  T2T_REQUIRE(H > 0 && N > 0 && CQ > 0, "tile_attn_run_planned: H=%d N=%d CQ=%d", H, N, CQ);
+  T2T_REQUIRE(H > 0 && N > 0 && N < (1 << 24) && CQ > 0, "tile_attn_run_planned: H=%d N=%d CQ=%d", H, N, CQ);
   hipStream_t st = (hipStream_t)stream;
   if (rebuild_plan) {
     const int rc = t2t_tile_plan(qcounts, kcounts, unip, plan, H, N, CQ, stream);
     if (rc) return rc;
   }
+  const size_t need = t2t_tile_attn_ws_bytes(H, N, dtype);
+  if (!ws || ws_bytes < need) {
+    t2t_set_error("tile_attn_run_planned: workspace of %zu bytes, need %zu", ws_bytes, need);
+    return T2T_ERR_WORKSPACE;
+  }
+  float* lse = (float*)ws;
+  void* tiles = (char*)ws + t2t_align256((size_t)H * N * sizeof(float));
   PlanView p = plan_view(plan, H, N, CQ);
+  launch_centroid_tiles(cks, sumv, tiles, H, st);
   if (dtype == T2T_F16)
-    launch_attn<F16T, true>(q, kp, vp, unip, qperm, kcounts, p, nullptr, nullptr, QU, cks, sumv,
-                            lam, tailw_dev, out, H, N, CQ, st);
+    launch_attn<F16T, 1>(q, kp, vp, unip, qperm, kcounts, p, nullptr, lse, out, H, N, CQ, st);
   else
-    launch_attn<BF16T, true>(q, kp, vp, unip, qperm, kcounts, p, nullptr, nullptr, QU, cks, sumv,
-                             lam, tailw_dev, out, H, N, CQ, st);
+    launch_attn<BF16T, 1>(q, kp, vp, unip, qperm, kcounts, p, nullptr, lse, out, H, N, CQ, st);
+  launch_resid<false>(dtype, nullptr, lse, QU, tiles, kcounts, unip, qlab, qperm, lam, tailw_dev,
+                      out, H, N, CQ, st);
   T2T_LAUNCH_CHECK("tile_attn_run_planned");
   return T2T_OK;
 }

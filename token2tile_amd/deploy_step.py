@@ -172,6 +172,9 @@ class MaskedStepDeploy:
         self._ws_kmm = torch.empty(ops.kmm_ws_bytes(H, N, CQ, C), dtype=torch.uint8, device=dev)
         self._ws_vst = torch.empty(ops.vstats_ws_bytes(H, N, C), dtype=torch.uint8, device=dev)
         self._ws_sel = torch.empty(ops.select_ws_bytes(H, N, CQ), dtype=torch.uint8, device=dev)
+        # lse and the centroid tile image of the attention call (dtype-independent size)
+        self._ws_attn = torch.empty(ops.attn_ws_bytes(H, N, torch.bfloat16), dtype=torch.uint8,
+                                    device=dev)
 
         self.cfg_reuse = bool(cfg_reuse)
         self.mask_refresh = max(1, int(mask_refresh))
@@ -369,7 +372,8 @@ class MaskedStepDeploy:
             with self._stage("attention"):
                 ops.tile_attn_run_planned(q, io["kp"], io["vp"], tile_sizes, counts, unip,
                                           self.QU, cks, self._kmm_sumv, self._kmm_lam, qlab_cur,
-                                          qperm, self.tailw_t, io["out"], plan, False, stream=s0)
+                                          qperm, self.tailw_t, io["out"], plan, False,
+                                          ws=self._ws_attn, stream=s0)
         s1.wait_stream(s0)
         cur = torch.cuda.current_stream(self.dev)
         cur.wait_stream(s0)

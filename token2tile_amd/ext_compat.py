@@ -104,6 +104,7 @@ class TileAttnExt:
 
     def __init__(self):
         self._plans = {}
+        self._ws = _WsCache()
 
     def _plan_for(self, plan, H, N, CQ):
         need = ops.plan_ints(H, N, CQ)
@@ -126,9 +127,10 @@ class TileAttnExt:
                     qperm, tailw_t, out, plan, rebuild):
         H, N, _ = q.shape
         CQ = tile_sizes.shape[1]
+        ws = self._ws.get((q.device, H, N), ops.attn_ws_bytes(H, N, q.dtype), q.device)
         ops.tile_attn_run_planned(q, kp, vp, tile_sizes, counts, self._packed(union_bits), QU, cks,
                                   sumv, lam, qlab, qperm, tailw_t, out,
-                                  self._plan_for(plan, H, N, CQ), bool(rebuild))
+                                  self._plan_for(plan, H, N, CQ), bool(rebuild), ws=ws)
         return out
 
     def run(self, q, kp, vp, tile_sizes, counts, union_bits, QU, cks, sumv, lam, qlab, qperm,

@@ -207,7 +207,7 @@ def tile_plan(qcounts, kcounts, unip, N, plan=None, stream=None):
 
 def plan_views(plan, H, N, CQ):
     """Named views of a plan buffer (k_off, kvlen, ntask, tasks)."""
-    maxT = CQ + (N + 127) // 128 + 1
+    maxT = CQ + (N + 127) // 128 + 1  # tasks of <= 128 queries
     o = 0
     k_off = plan[o:o + H * 2049].view(H, 2049); o += H * 2049
     kvlen = plan[o:o + H * CQ].view(H, CQ); o += H * CQ
@@ -229,12 +229,15 @@ def tile_attn_exact(q, kp, vp, kcounts, unip, qperm, plan, attn_out=None, lse=No
 
 
 def tail_merge(attn_out, lse, QU, cks, sumv, kcounts, unip, qlab, qperm, lam, tailw_t, out=None,
-               stream=None):
+               ws=None, stream=None):
     H, N, D = attn_out.shape
     CQ = unip.shape[1]
     out = torch.empty_like(attn_out) if out is None else out
+    need = size_query("t2t_tail_merge_ws_bytes", H)
+    if ws is None or ws.numel() < need:
+        ws = _ws(need, _dev(attn_out))
     call("t2t_tail_merge", attn_out, lse, QU, cks, sumv, kcounts, unip, qlab, qperm, lam, tailw_t,
-         out, dtype_code(attn_out.dtype), H, N, CQ, stream_handle(stream))
+         out, dtype_code(attn_out.dtype), H, N, CQ, ws, ws.numel(), stream_handle(stream))
     return out
 
 
@@ -246,9 +249,12 @@ def tile_attn_run_planned(q, kp, vp, qcounts, kcounts, unip, QU, cks, sumv, lam,
                           tailw_t, out, plan, rebuild, ws=None, stream=None):
     H, N, D = q.shape
     CQ = qcounts.shape[1]
+    need = attn_ws_bytes(H, N, q.dtype)
+    if ws is None or ws.numel() < need:
+        ws = _ws(need, _dev(q))
     call("t2t_tile_attn_run_planned", q, kp, vp, dtype_code(q.dtype), qcounts, kcounts, unip, QU,
-         cks, sumv, lam, qlab, qperm, tailw_t, out, plan, int(bool(rebuild)), H, N, CQ, None, 0,
-         stream_handle(stream))
+         cks, sumv, lam, qlab, qperm, tailw_t, out, plan, int(bool(rebuild)), H, N, CQ, ws,
+         ws.numel(), stream_handle(stream))
     return out
 
 
