@@ -183,6 +183,23 @@ int t2t_tail_merge(const void* attn_out, const float* lse, const void* QU,
                    const int32_t* qperm, const float* lam, const float* tailw_dev,
                    void* out, int dtype, int H, int N, int CQ,
                    void* ws, size_t ws_bytes, void* stream);
+/* The centroid tile image of one call: cks [H, 2048, 32] fp16 and sumv
+ * [H, 2048, 128] fp16 -> tiles (t2t_centroid_tiles_bytes(H) bytes).  Part of
+ * launch_tail_merge's staging, tile_attn/src/kernel.cu:1172-1250. */
+int t2t_centroid_tiles(const void* cks, const void* sumv, void* tiles, int H, void* stream);
+/* t2t_tile_attn_exact with the output at the ORIGINAL rows of out (lse still
+ * in sorted order), for the residual kernel to merge into in place. */
+int t2t_tile_attn_exact_orig(const void* q, const void* kp, const void* vp, int dtype,
+                             const int32_t* kcounts, const int32_t* unip, const int32_t* qperm,
+                             const int32_t* plan, void* out, float* lse,
+                             int H, int N, int CQ, void* stream);
+/* Residual + merge into the exact part held at the original rows of out
+ * (S6); tiles from t2t_centroid_tiles.  With the two entries above, the
+ * steps of t2t_tile_attn_run_planned one launch at a time. */
+int t2t_resid_merge_inplace(void* out, const float* lse, const void* QU, const void* tiles,
+                            const int32_t* kcounts, const int32_t* unip, const int32_t* qlab,
+                            const int32_t* qperm, const float* lam, const float* tailw_dev,
+                            int dtype, int H, int N, int CQ, void* stream);
 /* Workspace bytes of t2t_tile_attn_run_planned: lse [H, N] fp32 and the
  * centroid tile image. */
 size_t t2t_tile_attn_ws_bytes(int H, int N, int dtype);

@@ -46,6 +46,11 @@ SIGNATURES = {
     "t2t_tile_attn_exact": (c_int, [_P, _P, _P, c_int, _P, _P, _P, _P, _P, _P, c_int, c_int,
                                     c_int, _P]),
     "t2t_centroid_tiles_bytes": (c_size_t, [c_int]),
+    "t2t_centroid_tiles": (c_int, [_P, _P, _P, c_int, _P]),
+    "t2t_tile_attn_exact_orig": (c_int, [_P, _P, _P, c_int, _P, _P, _P, _P, _P, _P, c_int, c_int,
+                                         c_int, _P]),
+    "t2t_resid_merge_inplace": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int,
+                                        c_int, c_int, _P]),
     "t2t_tail_merge_ws_bytes": (c_size_t, [c_int]),
     "t2t_tail_merge": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int,
                                c_int, c_int, _P, c_size_t, _P]),

@@ -206,11 +206,15 @@ extern "C" int t2t_tile_plan(const int32_t* qcounts, const int32_t* kcounts, con
 // ---------------------------------------------------------------------------
 __device__ inline uint32_t pack2(uint16_t a, uint16_t b) { return (uint32_t)a | ((uint32_t)b << 16); }
 
-// map a linear block id to a task so that each XCD (8 of them, blocks are
-// dealt round-robin) works through a contiguous range of the task list
+// map a linear block id to a task: blocks are dealt to the 8 XCDs round
+// robin, so groups of 8 consecutive tasks (the tasks of one query cluster sit
+// next to each other in the task list) run on one XCD and share its L2, while
+// all XCDs sweep the task list together and keep to the same head's K/V in the
+// shared last-level cache.  The grid is a multiple of 64 blocks.
 __device__ inline int xcd_remap(int bid, int total) {
-  const int per = (total + 7) / 8;
-  return (bid % 8) * per + bid / 8;
+  (void)total;
+  const int r = bid / 8;
+  return (r / 8) * 64 + (bid % 8) * 8 + r % 8;
 }
 
 #define TA_MARGIN 3.0f   // log2 units of headroom when the exact-part max advances
@@ -555,7 +559,7 @@ static void launch_attn(const void* q, const void* kp, const void* vp, const int
                         void* attn_out, float* lse, void* out, int H, int N, int CQ,
                         hipStream_t st) {
   const int total = H * p.maxT;
-  const int grid = ((total + 7) / 8) * 8;
+  const int grid = ((total + 63) / 64) * 64;
   hipLaunchKernelGGL((attn_kernel<T, MODE>), dim3(grid), dim3(TA_WAVES * 64), 0, st,
                      (const uint16_t*)q, (const uint16_t*)kp, (const uint16_t*)vp,
                      (const uint32_t*)unip, qperm, kcounts, p.k_off, p.ntask, p.tasks,
@@ -840,6 +844,50 @@ extern "C" int t2t_tail_merge(const void* attn_out, const float* lse, const void
   launch_resid<true>(dtype, attn_out, lse, QU, ws, kcounts, unip, qlab, qperm, lam, tailw_dev, out,
                      H, N, CQ, st);
   T2T_LAUNCH_CHECK("tail_merge");
+  return T2T_OK;
+}
+
+extern "C" int t2t_centroid_tiles(const void* cks, const void* sumv, void* tiles, int H,
+                                  void* stream) {
+  T2T_REQUIRE(cks && sumv && tiles, "centroid_tiles: null pointer");
+  T2T_REQUIRE(H > 0, "centroid_tiles: H=%d", H);
+  launch_centroid_tiles(cks, sumv, tiles, H, (hipStream_t)stream);
+  T2T_LAUNCH_CHECK("centroid_tiles");
+  return T2T_OK;
+}
+
+extern "C" int t2t_tile_attn_exact_orig(const void* q, const void* kp, const void* vp, int dtype,
+                                        const int32_t* kcounts, const int32_t* unip,
+                                        const int32_t* qperm, const int32_t* plan, void* out,
+                                        float* lse, int H, int N, int CQ, void* stream) {
+  T2T_REQUIRE(q && kp && vp && kcounts && unip && qperm && plan && out && lse,
+              "tile_attn_exact_orig: null pointer");
+  T2T_REQUIRE(check_dtype(dtype), "tile_attn_exact_orig: dtype %d", dtype);
+  T2T_REQUIRE(H > 0 && N > 0 && N < (1 << 24) && CQ > 0, "tile_attn_exact_orig: H=%d N=%d CQ=%d",
+              H, N, CQ);
+  PlanView p = plan_view((int32_t*)plan, H, N, CQ);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == T2T_F16)
+    launch_attn<F16T, 1>(q, kp, vp, unip, qperm, kcounts, p, nullptr, lse, out, H, N, CQ, st);
+  else
+    launch_attn<BF16T, 1>(q, kp, vp, unip, qperm, kcounts, p, nullptr, lse, out, H, N, CQ, st);
+  T2T_LAUNCH_CHECK("tile_attn_exact_orig");
+  return T2T_OK;
+}
+
+extern "C" int t2t_resid_merge_inplace(void* out, const float* lse, const void* QU,
+                                       const void* tiles, const int32_t* kcounts,
+                                       const int32_t* unip, const int32_t* qlab,
+                                       const int32_t* qperm, const float* lam,
+                                       const float* tailw_dev, int dtype, int H, int N, int CQ,
+                                       void* stream) {
+  T2T_REQUIRE(out && lse && QU && tiles && kcounts && unip && qlab && qperm && lam && tailw_dev,
+              "resid_merge_inplace: null pointer");
+  T2T_REQUIRE(check_dtype(dtype), "resid_merge_inplace: dtype %d", dtype);
+  T2T_REQUIRE(H > 0 && N > 0 && CQ > 0, "resid_merge_inplace: H=%d N=%d CQ=%d", H, N, CQ);
+  launch_resid<false>(dtype, nullptr, lse, QU, tiles, kcounts, unip, qlab, qperm, lam, tailw_dev,
+                      out, H, N, CQ, (hipStream_t)stream);
+  T2T_LAUNCH_CHECK("resid_merge_inplace");
   return T2T_OK;
 }
 

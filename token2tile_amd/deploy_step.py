@@ -172,9 +172,11 @@ class MaskedStepDeploy:
         self._ws_kmm = torch.empty(ops.kmm_ws_bytes(H, N, CQ, C), dtype=torch.uint8, device=dev)
         self._ws_vst = torch.empty(ops.vstats_ws_bytes(H, N, C), dtype=torch.uint8, device=dev)
         self._ws_sel = torch.empty(ops.select_ws_bytes(H, N, CQ), dtype=torch.uint8, device=dev)
-        # lse and the centroid tile image of the attention call (dtype-independent size)
-        self._ws_attn = torch.empty(ops.attn_ws_bytes(H, N, torch.bfloat16), dtype=torch.uint8,
-                                    device=dev)
+        # attention call scratch: lse of the exact part (sorted order) and the
+        # centroid tile image the residual kernel stages from
+        self._lse = torch.empty(H, N, dtype=torch.float32, device=dev)
+        self._ctiles = torch.empty(ops.size_query("t2t_centroid_tiles_bytes", H), dtype=torch.uint8,
+                                   device=dev)
 
         self.cfg_reuse = bool(cfg_reuse)
         self.mask_refresh = max(1, int(mask_refresh))
@@ -369,11 +371,15 @@ class MaskedStepDeploy:
             if rebuild:
                 with self._stage("plan"):
                     ops.tile_plan(tile_sizes, counts, unip, N, plan=plan, stream=s0)
-            with self._stage("attention"):
-                ops.tile_attn_run_planned(q, io["kp"], io["vp"], tile_sizes, counts, unip,
-                                          self.QU, cks, self._kmm_sumv, self._kmm_lam, qlab_cur,
-                                          qperm, self.tailw_t, io["out"], plan, False,
-                                          ws=self._ws_attn, stream=s0)
+            # the steps of t2t_tile_attn_run_planned, one launch per stage
+            with self._stage("attention_prep"):
+                ops.centroid_tiles(cks, self._kmm_sumv, tiles=self._ctiles, stream=s0)
+            with self._stage("attention_exact"):
+                ops.tile_attn_exact_orig(q, io["kp"], io["vp"], counts, unip, qperm, plan,
+                                         io["out"], self._lse, stream=s0)
+            with self._stage("attention_residual"):
+                ops.resid_merge_inplace(io["out"], self._lse, self.QU, self._ctiles, counts, unip,
+                                        qlab_cur, qperm, self._kmm_lam, self.tailw_t, stream=s0)
         s1.wait_stream(s0)
         cur = torch.cuda.current_stream(self.dev)
         cur.wait_stream(s0)

@@ -241,6 +241,34 @@ def tail_merge(attn_out, lse, QU, cks, sumv, kcounts, unip, qlab, qperm, lam, ta
     return out
 
 
+def centroid_tiles(cks, sumv, tiles=None, stream=None):
+    """Tile image of cks / sumv staged by the residual kernel (uint8 bytes)."""
+    H = cks.shape[0]
+    need = size_query("t2t_centroid_tiles_bytes", H)
+    tiles = _ws(need, _dev(cks)) if tiles is None else tiles
+    call("t2t_centroid_tiles", cks, sumv, tiles, H, stream_handle(stream))
+    return tiles
+
+
+def tile_attn_exact_orig(q, kp, vp, kcounts, unip, qperm, plan, out, lse, stream=None):
+    """Exact attention written at the original rows of out; lse in sorted order."""
+    H, N, D = q.shape
+    CQ = unip.shape[1]
+    call("t2t_tile_attn_exact_orig", q, kp, vp, dtype_code(q.dtype), kcounts, unip, qperm, plan,
+         out, lse, H, N, CQ, stream_handle(stream))
+    return out
+
+
+def resid_merge_inplace(out, lse, QU, tiles, kcounts, unip, qlab, qperm, lam, tailw_t,
+                        stream=None):
+    """Residual + merge into the exact part held at the original rows of out."""
+    H, N, D = out.shape
+    CQ = unip.shape[1]
+    call("t2t_resid_merge_inplace", out, lse, QU, tiles, kcounts, unip, qlab, qperm, lam, tailw_t,
+         dtype_code(out.dtype), H, N, CQ, stream_handle(stream))
+    return out
+
+
 def attn_ws_bytes(H, N, dtype):
     return size_query("t2t_tile_attn_ws_bytes", H, N, dtype_code(dtype))
 
