@@ -131,6 +131,15 @@ int t2t_select_run_split_packed(const void* gl, const int32_t* kcounts,
                                 int32_t* unip, int32_t* rowcnt,
                                 int H, int N, int CQ,
                                 void* ws, size_t ws_bytes, void* stream);
+/* Scoring and selection in one pass (S3 + S4): the scores fp16(QU . cks^T)
+ * are computed on chip, with the arithmetic of t2t_score, and never stored;
+ * unip and rowcnt are bit-identical to t2t_score followed by
+ * t2t_select_run_packed.  Replaces torch.bmm(QU, cks^T, out=gl) +
+ * ext.run_packed, operator/deploy_step.py:393-411.  ws as for the selection. */
+int t2t_score_select_packed(const void* QU, const void* cks, const int32_t* kcounts,
+                            const int32_t* qperm, const int32_t* qcounts,
+                            const int32_t* ns_dev, int32_t* unip, int32_t* rowcnt,
+                            int H, int N, int CQ, void* ws, size_t ws_bytes, void* stream);
 /* Byte-per-cluster union uni[h, t, c] in {0, 1}, [H, CQ, CK] uint8.
  * Replaces ext.run, select_union/src/main.cpp:5-19 (kernel.cu:414-440). */
 int t2t_select_run(const void* gl, const int32_t* kcounts,

@@ -132,6 +132,45 @@ def test_select_union_bit_exact(dev, kind, ns):
     assert np.array_equal(c(ub).astype(bool), O.unpack_bits(eu))
 
 
+FUSED_CASES = ["normal", "tied_centroids", "zeros", "one_per_cluster"]
+
+
+@pytest.mark.parametrize("kind", FUSED_CASES)
+@pytest.mark.parametrize("ns", [1, 300, 3333])
+def test_score_select_fused_matches_split(dev, kind, ns):
+    """The fused scoring + selection equals t2t_score + t2t_select_run_packed
+    bit for bit, and the selection matches the oracle on those scores."""
+    from token2tile_amd import ops
+    rng = np.random.default_rng(hash(("fused", kind, ns)) % (2 ** 32))
+    H, N, CQ = 2, 3333, 24                      # N not a multiple of the 128-row block
+    QU = rng.normal(0, 1, (H, N, 32)).astype(np.float16)
+    ck2 = rng.normal(0, 0.5, (H, 2048, 32)).astype(np.float32)
+    if kind == "tied_centroids":                 # duplicated centroids -> exactly tied scores
+        ck2[:, 1024:] = ck2[:, :1024]
+    sizes = np.stack([rng.multinomial(N, np.ones(2048) / 2048) for _ in range(H)]).astype(np.int32)
+    if kind == "zeros":                         # 1500 empty key clusters, same key total
+        for h in range(H):
+            z = rng.choice(2048, 1500, replace=False)
+            moved = sizes[h, z].sum()
+            sizes[h, z] = 0
+            sizes[h, rng.choice(np.setdiff1d(np.arange(2048), z))] += moved
+    if kind == "one_per_cluster":
+        CQ = 512
+        qlab = np.stack([rng.permutation(N) % CQ for _ in range(H)]).astype(np.int32)
+    else:
+        qlab = rng.integers(0, CQ - 1, (H, N)).astype(np.int32)   # cluster CQ-1 stays empty
+    qperm, qcounts = O.stable_perm(qlab, CQ)
+    _, cks = ops.centroid_finalize(g(ck2, dev))
+    ns_t = torch.tensor(ns, dtype=torch.int32, device=dev)
+    gl = ops.score(g(QU, dev), cks)
+    u_split, r_split = ops.select_union(gl, g(sizes, dev), g(qperm, dev), g(qcounts, dev), ns_t)
+    u_fused, r_fused = ops.score_select(g(QU, dev), cks, g(sizes, dev), g(qperm, dev),
+                                        g(qcounts, dev), ns_t)
+    assert torch.equal(u_fused, u_split) and torch.equal(r_fused, r_split)
+    eu, er = O.select_union(c(gl), sizes, qperm, qcounts, ns)
+    assert np.array_equal(c(u_fused), eu) and np.array_equal(c(r_fused), er)
+
+
 def test_select_one_query_per_cluster_and_full_budget(dev):
     from token2tile_amd import ops
     rng = np.random.default_rng(9)

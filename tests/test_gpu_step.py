@@ -57,7 +57,8 @@ def test_full_call_matches_oracle(dev, dtype):
     qperm = last["qperm"].cpu().numpy()
     kcounts = last["counts"].cpu().numpy()
     qcounts = last["tile_sizes"].cpu().numpy()
-    gl = deploy.gl.cpu().numpy()
+    from token2tile_amd import ops
+    gl = ops.score(deploy.QU, last["cks"]).cpu().numpy()  # the scores the fused kernel used
     eu, er = O.select_union(gl, kcounts, qperm, qcounts, deploy.ns)
     assert np.array_equal(unip, eu)
     assert np.array_equal(deploy.rowcnt.cpu().numpy(), er)

@@ -34,6 +34,8 @@ SIGNATURES = {
     "t2t_centroid_finalize": (c_int, [_P, _P, _P, c_float, c_int, c_int, c_int, _P]),
     "t2t_score": (c_int, [_P, _P, _P, c_int, c_int, c_int, c_int, _P]),
     "t2t_select_ws_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "t2t_score_select_packed": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, _P,
+                                        c_size_t, _P]),
     "t2t_select_run_packed": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, _P,
                                       c_size_t, _P]),
     "t2t_select_run_split_packed": (c_int, [_P, _P, _P, _P, c_int, _P, _P, _P, c_int, c_int,

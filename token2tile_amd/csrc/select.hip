@@ -241,6 +241,137 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
   flush_union(acc, uh + (size_t)t * (SEL_NC / 32));
 }
 
+// ---------------------------------------------------------------------------
+// Fused scoring + selection: the scores never leave the chip.  One 8-wave
+// work-group per CU takes batches of 32 consecutive sorted rows: every wave
+// computes the scores of the batch against 256 of the centroids on MFMA, with
+// the instruction, operand split and fp16 rounding of score_kernel (so the
+// scores, and the selection, are bit-identical to the unfused path), and
+// stores the ordered keys in LDS; then every wave selects 4 of the rows.
+// ---------------------------------------------------------------------------
+#define SF_WAVES 8
+#define SF_ROWS 32
+#define SF_BATCHES 4
+#define SF_PITCH (SEL_NC + 8)  // halves per LDS key row (16-byte aligned rows)
+
+__global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
+    const uint16_t* __restrict__ QU, const uint16_t* __restrict__ cks,
+    const int32_t* __restrict__ kcounts, const int32_t* __restrict__ qperm,
+    const int32_t* __restrict__ off, const int32_t* __restrict__ ns_dev,
+    int32_t* __restrict__ unip, int32_t* __restrict__ rowcnt, int N, int CQ) {
+  __shared__ __attribute__((aligned(16))) uint16_t sKey[SF_ROWS * SF_PITCH];
+  __shared__ int hist_all[SF_WAVES][256];
+  const int h = blockIdx.y;
+  const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int jl = l & 31, hh = l >> 5;
+  int* hist = hist_all[wv];
+  const int32_t* offh = off + (size_t)h * (CQ + 1);
+  int lim = offh[CQ];
+  if (lim > N) lim = N;  // qcounts summing past N is invalid input; never read past N
+  const int base = blockIdx.x * SF_ROWS * SF_BATCHES;
+  if (base >= lim) return;
+  // cluster sizes of the lane's 32 selection clusters, and the key total
+  int sz[32];
+  int ktot = 0;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int32_t* p = kcounts + (size_t)h * SEL_NC + 512 * g + 8 * l;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      sz[8 * g + j] = p[j];
+      ktot += p[j];
+    }
+  }
+  ktot = wave_sum(ktot);
+  int ns = *ns_dev;
+  ns = ns < 1 ? 1 : ns;
+  ns = ns > ktot ? ktot : ns;
+  // centroid fragments of the wave's 256 centroids (the A operands of
+  // score_kernel: row 32 cb + jl, dims 8 hh .. and 16 + 8 hh ..)
+  u32x4 ca0[8], ca1[8];
+  {
+    const uint16_t* ch = cks + ((size_t)h * SEL_NC + 256 * wv + jl) * 32 + 8 * hh;
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb) {
+      ca0[cb] = *(const u32x4*)(ch + cb * 32 * 32);
+      ca1[cb] = *(const u32x4*)(ch + cb * 32 * 32 + 16);
+    }
+  }
+  const int32_t* qp = qperm + (size_t)h * N;
+  const uint16_t* qh = QU + (size_t)h * N * 32;
+  int32_t* uh = unip + (size_t)h * CQ * (SEL_NC / 32);
+  int t = -1, tend = 0;
+  uint32_t acc = 0;
+  for (int b = 0; b < SF_BATCHES; ++b) {
+    const int j0 = base + SF_ROWS * b;
+    if (j0 >= lim) break;
+    {  // scores of rows j0 .. j0 + 31 against the wave's centroids -> keys in LDS
+      const int row = j0 + jl;
+      u32x4 b0 = {0u, 0u, 0u, 0u}, b1 = {0u, 0u, 0u, 0u};
+      if (row < lim) {
+        const uint16_t* qr = qh + (size_t)qp[row] * 32 + 8 * hh;
+        b0 = *(const u32x4*)(qr);
+        b1 = *(const u32x4*)(qr + 16);
+      }
+      uint16_t* krow = sKey + jl * SF_PITCH + 256 * wv + 4 * hh;
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb) {
+        f32x16 sc = zero16();
+        sc = Mfma<F16T>::run(ca0[cb], b0, sc);
+        sc = Mfma<F16T>::run(ca1[cb], b1, sc);
+        // lane holds centroids 32 cb + 8 g + 4 hh + e (e < 4) of row jl
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          u32x2 o;
+          o[0] = (uint32_t)f2h(sc[4 * g + 0]) | ((uint32_t)f2h(sc[4 * g + 1]) << 16);
+          o[1] = (uint32_t)f2h(sc[4 * g + 2]) | ((uint32_t)f2h(sc[4 * g + 3]) << 16);
+#pragma unroll
+          for (int w = 0; w < 2; ++w)  // ordered keys of both halves
+            o[w] ^= ((o[w] >> 15) & 0x00010001u) * 0x7FFFu;
+          *(u32x2*)(krow + 32 * cb + 8 * g) = o;
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int i = 0; i < SF_ROWS / SF_WAVES; ++i) {
+      const int r = (SF_ROWS / SF_WAVES) * wv + i;
+      const int j = j0 + r;
+      if (j >= lim) break;  // wave-uniform
+      if (j >= tend) {      // wave-uniform: every lane takes part in the shuffles
+        if (t >= 0) flush_union(acc, uh + (size_t)t * (SEL_NC / 32));
+        acc = 0;
+        if (t < 0) {  // query cluster of the first row: largest t with off[t] <= j
+          int lo = 0, hi = CQ - 1;
+          while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (offh[mid] <= j) lo = mid; else hi = mid - 1;
+          }
+          t = lo;
+        }
+        while (t < CQ - 1 && offh[t + 1] <= j) ++t;  // next non-empty cluster
+        tend = offh[t + 1];
+      }
+      int key[32];
+      const uint16_t* kr = sKey + r * SF_PITCH;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const u32x4 v = *(const u32x4*)(kr + 512 * g + 8 * l);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          key[8 * g + 2 * q] = (int)(int16_t)(uint16_t)(v[q] & 0xffffu);
+          key[8 * g + 2 * q + 1] = (int)(int16_t)(uint16_t)(v[q] >> 16);
+        }
+      }
+      int rc;
+      acc |= select_row(key, sz, hist, ns, &rc);
+      if (l == 0) rowcnt[(size_t)h * N + qp[j]] = rc;
+    }
+    __syncthreads();  // the next batch overwrites the keys
+  }
+  if (t >= 0) flush_union(acc, uh + (size_t)t * (SEL_NC / 32));
+}
+
 __global__ void expand_union_kernel(const int32_t* __restrict__ unip, uint8_t* __restrict__ uni,
                                     long long nbits) {
   for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < nbits;
@@ -276,6 +407,32 @@ static int select_common(const void* gl, const int32_t* kcounts, const int32_t* 
   hipLaunchKernelGGL(select_main_kernel, dim3(cdiv(N, rows_per_block), H), dim3(SEL_WAVES * 64), 0,
                      st, (const uint16_t*)gl, kcounts, qperm, off, ns_dev, unip, rowcnt, N, CQ);
   T2T_LAUNCH_CHECK("select_main");
+  return T2T_OK;
+}
+
+extern "C" int t2t_score_select_packed(const void* QU, const void* cks, const int32_t* kcounts,
+                                       const int32_t* qperm, const int32_t* qcounts,
+                                       const int32_t* ns_dev, int32_t* unip, int32_t* rowcnt,
+                                       int H, int N, int CQ, void* ws, size_t ws_bytes,
+                                       void* stream) {
+  T2T_REQUIRE(QU && cks && kcounts && qperm && qcounts && ns_dev && unip && rowcnt,
+              "score_select: null pointer");
+  T2T_REQUIRE(H > 0 && N > 0 && CQ > 0, "score_select: H=%d N=%d CQ=%d", H, N, CQ);
+  T2T_REQUIRE(N < 524288, "score_select: N=%d must be < 524288", N);
+  if (!ws || ws_bytes < t2t_select_ws_bytes(H, N, CQ)) {
+    t2t_set_error("score_select: workspace %zu < %zu bytes", ws_bytes,
+                  t2t_select_ws_bytes(H, N, CQ));
+    return T2T_ERR_WORKSPACE;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  WsCarver w(ws);
+  int32_t* off = w.take<int32_t>((size_t)H * (CQ + 1));
+  hipLaunchKernelGGL(select_prep_kernel, dim3(H), dim3(1024), 0, st, qcounts, off, unip, CQ);
+  T2T_LAUNCH_CHECK("score_select prep");
+  hipLaunchKernelGGL(score_select_kernel, dim3(cdiv(N, SF_ROWS * SF_BATCHES), H),
+                     dim3(SF_WAVES * 64), 0, st, (const uint16_t*)QU, (const uint16_t*)cks,
+                     kcounts, qperm, off, ns_dev, unip, rowcnt, N, CQ);
+  T2T_LAUNCH_CHECK("score_select");
   return T2T_OK;
 }
 

@@ -156,7 +156,6 @@ class MaskedStepDeploy:
         f16, f32, i32 = torch.float16, torch.float32, torch.int32
         self.QU = torch.empty(H, N, r, device=dev, dtype=f16)
         self.KU = torch.empty(H, N, r, device=dev, dtype=f16)
-        self.gl = torch.empty(H, N, C, device=dev, dtype=f16)
         self.klab = torch.empty(H, N, device=dev, dtype=i32)
         self.qlab = torch.empty(H, N, device=dev, dtype=i32)
         self.rowcnt = torch.empty(H, N, device=dev, dtype=i32)
@@ -337,13 +336,15 @@ class MaskedStepDeploy:
                     ck16, cks = ops.centroid_finalize(self._kmm_ck2, self.scale, stream=s0)
                     state["ck"] = ck16
                     state["cq"] = self._kmm_cq2.clone()
-                    ops.score(self.QU, cks, out=self.gl, stream=s0)
                 unip = held["unip"] if recycle else torch.empty(H, CQ, C // 32, device=self.dev,
                                                                 dtype=torch.int32)
+                # scores fp16(QU . cks^T) and the selection in one kernel: the
+                # [H, N, 2048] score tensor is never stored (the split variant
+                # of the reference yields the same bitmap, so split_cap has no
+                # effect here)
                 with self._stage("select"):
-                    ops.select_union(self.gl, counts, qperm, tile_sizes, self.ns_t, unip=unip,
-                                     rowcnt=self.rowcnt, ws=self._ws_sel,
-                                     split_cap=self.split_cap, stream=s0)
+                    ops.score_select(self.QU, cks, counts, qperm, tile_sizes, self.ns_t, unip=unip,
+                                     rowcnt=self.rowcnt, ws=self._ws_sel, stream=s0)
                     if self.pin_tail:
                         ops.union_or_last(unip, stream=s0)
                 with self._stage("gather_k"):

@@ -161,6 +161,25 @@ def select_union(gl, kcounts, qperm, qcounts, ns_t, unip=None, rowcnt=None, ws=N
     return unip, rowcnt
 
 
+def score_select(QU, cks, kcounts, qperm, qcounts, ns_t, unip=None, rowcnt=None, ws=None,
+                 stream=None):
+    """Fused scoring + selection: packed union [H, CQ, 64] int32 and rowcnt
+    [H, N], identical to score() followed by select_union()."""
+    H, N, r = QU.shape
+    CQ = qcounts.shape[1]
+    dev = _dev(QU)
+    if cks.shape != (H, C_KEYS, RANK):
+        raise ValueError("t2t: score_select requires cks [H, 2048, 32]")
+    unip = torch.empty(H, CQ, C_KEYS // 32, dtype=_i32, device=dev) if unip is None else unip
+    rowcnt = torch.empty(H, N, dtype=_i32, device=dev) if rowcnt is None else rowcnt
+    need = select_ws_bytes(H, N, CQ)
+    if ws is None or ws.numel() < need:
+        ws = _ws(need, dev)
+    call("t2t_score_select_packed", QU, cks, kcounts, qperm, qcounts, ns_t, unip, rowcnt, H, N, CQ,
+         ws, ws.numel(), stream_handle(stream))
+    return unip, rowcnt
+
+
 def select_union_bytes(gl, kcounts, qperm, qcounts, ns_t, uni=None, rowcnt=None, ws=None,
                        stream=None):
     """Byte-per-cluster union [H, CQ, 2048] uint8 (the reference's `run`)."""
