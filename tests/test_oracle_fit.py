@@ -34,6 +34,36 @@ def test_online_u_invariants():
         assert np.allclose(uq @ uk.T, Rqi.T @ best @ Rki.T, atol=1e-4)
 
 
+def fit_case():
+    rng = np.random.default_rng(0)
+    H, N, D, r = 2, 2000, 128, 32
+    A = rng.normal(0, 1, (D, D)) / np.sqrt(D)
+    q = (rng.normal(0, 1, (H, N, D)) @ A).astype(np.float32)
+    k = (rng.normal(0, 1, (H, N, D)) @ A.T + 0.1 * rng.normal(0, 1, (H, N, D))).astype(np.float32)
+    return q, k, r
+
+
+@pytest.mark.gpu
+def test_operator_online_u_invariants(dev):
+    """The operator's fit (Gram + eigh of M^T M on the GPU) satisfies the same
+    invariants and gives the oracle's product Uq Uk^T."""
+    import torch
+    from token2tile_amd.deploy_step import online_u
+    q, k, r = fit_case()
+    Uq, Uk = (t.cpu().numpy().astype(np.float64) for t in
+              online_u(torch.from_numpy(q).to(dev), torch.from_numpy(k).to(dev), r))
+    Oq, Ok = O.online_u(q, k, r)
+    N = q.shape[1]
+    for h in range(q.shape[0]):
+        qd, kd = q[h].astype(np.float64), k[h].astype(np.float64)
+        Mq, Mk = qd.T @ qd / N, kd.T @ kd / N
+        S = np.diag(Oq[h].astype(np.float64).T @ Mq @ Oq[h].astype(np.float64))
+        assert np.allclose(Uq[h].T @ Mq @ Uq[h], np.diag(S), atol=2e-5 * S[0])
+        assert np.allclose(Uk[h].T @ Mk @ Uk[h], np.diag(S), atol=2e-5 * S[0])
+        assert np.allclose(Uq[h] @ Uk[h].T, Oq[h].astype(np.float64) @ Ok[h].astype(np.float64).T,
+                           atol=1e-4)
+
+
 def test_online_u_rejects_nonfinite():
     q = np.zeros((1, 10, 128), dtype=np.float32)
     q[0, 3, 4] = np.nan
