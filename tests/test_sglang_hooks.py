@@ -1,0 +1,78 @@
+"""SGLang-side hooks (integrations/sglang/token2tile_sglang.patch): the gfx950
+resolver gate, the denoising metadata branch and the H3 layout record, which
+the H3 path then reads."""
+import pytest
+import torch
+
+from token2tile_amd.backend import sglang_hooks as S
+from token2tile_amd.backend import t2t_attn as B
+
+
+class _Platform:
+    def __init__(self, arch):
+        self.arch = arch
+
+    def get_device_arch(self):
+        return self.arch
+
+
+def test_resolver_gates_on_gfx950():
+    assert S.resolve_backend(arch="gfx950") == S.BACKEND_PATH
+    assert S.resolve_backend(_Platform("gfx950:sramecc+:xnack-")) == S.BACKEND_PATH
+    for bad in ("gfx942", "gfx90a", "", None):
+        with pytest.raises(ValueError, match="gfx950"):
+            S.resolve_backend(_Platform(bad))
+    # the path names an importable class with the backend surface
+    mod, cls = S.BACKEND_PATH.rsplit(".", 1)
+    backend = getattr(__import__(mod, fromlist=[cls]), cls)
+    assert backend is B.T2TAttentionBackend
+    assert backend.get_impl_cls() is B.T2TAttentionImpl
+
+
+def test_denoising_metadata_keeps_one_cache_per_request():
+    builder = B.T2TAttentionMetadataBuilder()
+    cfg = {"t2t_profile": "manual", "t2t_ns_base": 300, "t2t_dense_prefix_steps": 2,
+           "t2t_cq": 32, "t2t_ck": 2048, "t2t_step_profile": [1, 1, 1, 1],
+           "t2t_layer_profile": [1] * 6, "t2t_cfg_mult": [1.0, 0.5], "t2t_mask_refresh": 2}
+    extra = {}
+    steps = list(range(20))
+    m0 = S.build_denoising_metadata(builder, cfg, extra, 0, steps)
+    m5 = S.build_denoising_metadata(builder, cfg, extra, 5, steps)
+    assert m0.cache is m5.cache is extra["t2t_cache"]
+    assert (m5.step_index, m5.total_steps, m5.profile_name, m5.ns_base) == (5, 20, "manual", 300)
+    assert m5.cfg_mult == (1.0, 0.5) and m5.mask_refresh == 2 and m5.cfg_reuse is True
+    other = {}
+    assert S.build_denoising_metadata(builder, cfg, other, 0, steps).cache is not m0.cache
+    d = S.build_denoising_metadata(builder, None, {}, 3, steps)
+    assert d.profile_name == "auto" and d.ns_base is None and d.warm_iters == 4
+    with pytest.raises(ValueError, match="timesteps"):
+        S.build_denoising_metadata(builder, cfg, {}, 0, None)
+
+
+def test_h3_layout_record_drives_the_varlen_rules():
+    # packed [text 40 | keyframes 100 | audio 60 | generated video 500]
+    text = torch.arange(0, 40)
+    key = torch.arange(40, 140)
+    audio = torch.arange(140, 200)
+    gen = torch.arange(200, 700)
+    lay = S.minimax_h3_layout(torch.cat((key, gen)), audio, text)
+    assert lay == {"video_tail": 500, "video": 600, "video_start": 40, "video_stop": 700,
+                   "audio": 60, "text_rows": 40}
+    assert B._h3_video_tokens_from_layout(700, lay) == 500
+    video, (vid, ctx) = B._h3_cond_sparse_rows(700, "cpu", lay)
+    assert video == 600
+    assert torch.equal(vid, torch.cat((key, gen)))
+    assert torch.equal(ctx, torch.cat((text, audio)))
+    # no keyframes: video follows the audio and the whole image segment is the tail
+    lay2 = S.minimax_h3_layout(gen, audio, text)
+    assert lay2["video_tail"] == lay2["video"] == 500
+    assert B._h3_video_tokens_from_layout(700, lay2) == 500
+    assert B._h3_cond_sparse_rows(700, "cpu", lay2) is None
+    empty = S.minimax_h3_layout(torch.empty(0, dtype=torch.long), audio, text)
+    assert empty["video"] == 0 and empty["video_start"] == -1
+
+
+@pytest.mark.gpu
+def test_resolver_on_this_device(dev):
+    assert S.device_arch() == "gfx950"
+    assert S.resolve_backend() == S.BACKEND_PATH
