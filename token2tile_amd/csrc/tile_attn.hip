@@ -230,11 +230,19 @@ typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 // LDS tile layouts (no padding, XOR swizzles keep the MFMA operand reads
 // conflict free):
 //   sK  [64 keys][128 dims]: 16-byte chunk c of row r lives at chunk c ^ (r & 15)
+//   sV  [64 keys][128 dims]: chunk c of row r at chunk c ^ sv_swz(r)
 //   sVt [128 dims][64 keys]: the 4-key granules a lane feeds to one MFMA
 //     (g = 4 m + h and 4 m + 2 + h) are stored side by side, so the operand is
 //     one 16-byte read: granule g sits in 16-byte unit (g & ~3) / 2 + (g & 1),
 //     half (g >> 1) & 1, and the unit is XOR-swizzled by ((d >> 1) ^ (d >> 4)) & 7
 __device__ inline int sk_off(int row, int chunk) { return row * 128 + 8 * (chunk ^ (row & 15)); }
+// sV [64 keys][128 dims], row-major, read only by the transposing reads: 16-byte
+// chunk c of key r lives at chunk c ^ sv_swz(r).  One such read has the 32 lanes
+// of a half-wave address 4 consecutive keys (r % 4 = 0..3) x chunk bits 0-1
+// (8-byte half by lane parity); moving r % 4 into chunk bits 2-3 puts the half-wave
+// on all 64 banks exactly once.  (The K swizzle, r & 15, would overlap r % 4 with
+// chunk bits 0-1 and leave the half-wave on 16 banks: 4-way conflicts.)
+__device__ inline int sv_swz(int row) { return (row & 3) << 2; }
 __device__ inline int vt_swz(int dim) { return ((dim >> 1) ^ (dim >> 4)) & 7; }
 __device__ inline int vt_unit_off(int dim, int unit) { return dim * 64 + 8 * (unit ^ vt_swz(dim)); }
 __device__ inline int vt_gran_off(int dim, int g) {
@@ -358,7 +366,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
           const int key = 16 * mm + 8 * r + trkey, dim = 32 * nb + trdim;
-          const uint16_t* src = sVb + key * 128 + 8 * ((dim >> 3) ^ (key & 15)) + (dim & 7);
+          const uint16_t* src = sVb + key * 128 + 8 * ((dim >> 3) ^ sv_swz(key)) + (dim & 7);
           part[r] = __builtin_bit_cast(
               u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)src));
         }
@@ -436,10 +444,12 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
       for (int i = 0; i < 4; ++i) {
         const int blk = 4 * i + wave;
         const int row = 4 * blk + (lane >> 4);
-        const uint32_t off = (uint32_t)sIdx[buf][row] * 256u + 16u * ((lane & 15) ^ (row & 15));
-        __builtin_amdgcn_global_load_lds((const glb_void_t*)(kh + off),
+        const uint32_t base = (uint32_t)sIdx[buf][row] * 256u;
+        const uint32_t offk = base + 16u * ((lane & 15) ^ (row & 15));
+        const uint32_t offv = base + 16u * ((lane & 15) ^ sv_swz(row));
+        __builtin_amdgcn_global_load_lds((const glb_void_t*)(kh + offk),
                                          (lds_void_t*)(sKb + blk * 4 * 128), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const glb_void_t*)(vh + off),
+        __builtin_amdgcn_global_load_lds((const glb_void_t*)(vh + offv),
                                          (lds_void_t*)(sVb + blk * 4 * 128), 16, 0, 0);
       }
     };
