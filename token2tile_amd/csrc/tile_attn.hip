@@ -250,6 +250,22 @@ __device__ inline int vt_gran_off(int dim, int g) {
 }
 
 __device__ inline float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+// bitfield insert: (m & a) | (~m & b), one v_bfi_b32.  Only ever applied to
+// values produced by ordinary VALU instructions (never straight to an MFMA
+// result: the compiler's wait states for reading MFMA results do not cover
+// inline assembly).
+__device__ inline uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+  return r;
+}
+// an fp16 pair with each half replaced by -inf where its bit of u is set
+// (bits `bit` and `bit` + 1 for the low and high half)
+__device__ inline uint32_t mask_pair_neg_inf(uint32_t pk, uint32_t u, int bit) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_sbfe((int)u, bit, 1);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_sbfe((int)u, bit + 1, 1);
+  return bfi(bfi(0x0000ffffu, lo, hi), 0xfc00fc00u, pk);
+}
 // (b.lo16 << 16) | a.lo16 and (b.hi16 << 16) | a.hi16
 __device__ inline uint32_t pack_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
 __device__ inline uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
@@ -678,28 +694,28 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
       nw1 = ur[2 * tc + 3];
     }
     // fp16 scores of the lane's query against centroids 32 kb + 8 (a / 4) +
-    // 4 hh + a % 4 of the tile; centroids in the query's union -> -inf
-    float sv[2][16];
+    // 4 hh + a % 4 of the tile, as pairs; centroids in the query's union ->
+    // -inf.  The union bit becomes an all-ones/zero word (opaque to the
+    // compiler, so the select stays one bitfield insert instead of a compare
+    // and a conditional move); the max runs on the packed pairs and the
+    // exponent argument reads the fp16 halves directly (v_fma_mix_f32).
+    f16x2 sp[2][8];
+    f16x2 mp = {(_Float16)-__builtin_inff(), (_Float16)-__builtin_inff()};
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int r = 32 * kb + jl;
       f32x16 S = zero16();
       S = Mfma<F16T>::run(*(const u32x4*)(sb + rc_off(r, hh)), qu0, S);
       S = Mfma<F16T>::run(*(const u32x4*)(sb + rc_off(r, 2 + hh)), qu1, S);
-      const uint32_t uw = kb ? uw1 : uw0;
+      const uint32_t u = (kb ? uw1 : uw0) >> (4 * hh);  // element a <-> bit 8 (a / 4) + a % 4
 #pragma unroll
       for (int a = 0; a < 16; a += 2) {
         const uint32_t pk = Pk<F16T>::pack(S[a], S[a + 1]);
-        const int b0 = 8 * (a / 4) + 4 * hh + (a % 4);
-        sv[kb][a] = ((uw >> b0) & 1u) ? -__builtin_inff() : h2f((uint16_t)(pk & 0xffffu));
-        sv[kb][a + 1] = ((uw >> (b0 + 1)) & 1u) ? -__builtin_inff() : h2f((uint16_t)(pk >> 16));
+        sp[kb][a / 2] = __builtin_bit_cast(f16x2, mask_pair_neg_inf(pk, u, 8 * (a / 4) + (a % 4)));
+        mp = __builtin_elementwise_maximum(mp, sp[kb][a / 2]);
       }
     }
-    float mx = -__builtin_inff();
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int a = 0; a < 16; a += 2) mx = vmax(mx, vmax(sv[kb][a], sv[kb][a + 1]));
+    float mx = vmax((float)mp[0], (float)mp[1]);
     mx = vmax(mx, __shfl_xor(mx, 32, 64));
     if (__builtin_amdgcn_readfirstlane((int)(__ballot(mx > m2) != 0ull))) {
       T2T_REAL_BRANCH();
@@ -722,7 +738,7 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
         float pe[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          pe[e] = __builtin_amdgcn_exp2f(fmaf(sv[kb][4 * j + e], L2E, nm));
+          pe[e] = __builtin_amdgcn_exp2f(fmaf((float)sp[kb][2 * j + e / 2][e % 2], L2E, nm));
           phi = fmaf(pe[e], cn[e], phi);
         }
         pb[2 * kb + j / 2][2 * (j % 2)] = Pk<F16T>::pack(pe[0], pe[1]);
