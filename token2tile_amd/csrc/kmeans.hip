@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void assign_kernel(const uint16_t* __restrict_
       }
     }
   }
-  if (MODE == 1) xsq += __shfl_xor(xsq, 32, 64);
+  if (MODE == 1) xsq = half_sum(xsq);
   const uint16_t* ch = cen + (size_t)h * C * D;
   const int Cp = (C + 31) & ~31;
   float best = __builtin_inff();
@@ -119,15 +119,15 @@ __global__ __launch_bounds__(256) void assign_kernel(const uint16_t* __restrict_
   }
   int lab;
   if (MODE == 0) {
-    const float ob = __shfl_xor(best, 32, 64);
-    const int oi = __shfl_xor(bidx, 32, 64);
+    const float ob = __builtin_bit_cast(float, half_partner(__builtin_bit_cast(uint32_t, best)));
+    const int oi = (int)half_partner((uint32_t)bidx);
     if (ob < best || (ob == best && oi < bidx)) {
       best = ob;
       bidx = oi;
     }
     lab = bidx;
   } else {
-    const int ok2 = __shfl_xor(bkey, 32, 64);
+    const int ok2 = (int)half_partner((uint32_t)bkey);
     bkey = ok2 < bkey ? ok2 : bkey;
     lab = bkey & ((1 << ibits) - 1);
   }

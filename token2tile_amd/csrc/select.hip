@@ -82,9 +82,9 @@ __device__ inline int find_cross(const int* hist, int base, int ns, int* above, 
   }
   const unsigned long long bal = __ballot(mine);
   const int src = bal ? (int)__ffsll((long long)bal) - 1 : 0;
-  *above = __shfl(ab, src, 64);
-  *inbin = __shfl(ib, src, 64);
-  return __shfl(bin, src, 64);
+  *above = __builtin_amdgcn_readlane(ab, src);
+  *inbin = __builtin_amdgcn_readlane(ib, src);
+  return __builtin_amdgcn_readlane(bin, src);
 }
 
 // Selection of one row.  keys/sz: the lane's 32 clusters (index 8 g + j).
@@ -149,7 +149,7 @@ __device__ inline uint32_t select_row(const int (&key)[32], const int (&sz)[32],
       }
       bits |= (uint32_t)s << i;
     }
-    before += __shfl(inc, 63, 64);
+    before += __builtin_amdgcn_readlane(inc, 63);
   }
   *rowcnt = wgt + wave_sum(took);
   return bits;
@@ -162,7 +162,10 @@ __device__ inline void flush_union(uint32_t acc, int32_t* urow) {
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const uint32_t b = (acc >> (8 * g)) & 0xffu;
-    const uint32_t b1 = __shfl_down(b, 1, 64), b2 = __shfl_down(b, 2, 64), b3 = __shfl_down(b, 3, 64);
+    // lanes 4q + 1 .. 4q + 3 of the quad (DPP quad_perm [1,1,1,1], [2,2,2,2], [3,3,3,3])
+    const uint32_t b1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)b, 0x55, 0xf, 0xf, false);
+    const uint32_t b2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)b, 0xaa, 0xf, 0xf, false);
+    const uint32_t b3 = (uint32_t)__builtin_amdgcn_mov_dpp((int)b, 0xff, 0xf, 0xf, false);
     const uint32_t w = b | (b1 << 8) | (b2 << 16) | (b3 << 24);
     if ((l & 3) == 0 && w) atomicOr((unsigned int*)&urow[16 * g + (l >> 2)], w);
   }

@@ -2,6 +2,7 @@
 // MFMA wrappers, wave64 reductions and host-side error plumbing.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <climits>
 #include <hip/hip_fp16.h>
 #include <hip/hip_bf16.h>
 #include <stdint.h>
@@ -115,19 +116,51 @@ __device__ inline f32x16 zero16() {
 // ---------------------------------------------------------------------------
 __device__ inline int lane_id() { return __lane_id(); }
 
-__device__ inline int wave_incl_scan(int v) {
-  const int l = __lane_id();
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    int y = __shfl_up(v, d, 64);
-    if (l >= d) v += y;
-  }
-  return v;
+// Cross-lane steps run on DPP (data-parallel primitives: a VALU operand read
+// from another lane of the same row of 16, or a row broadcast), not through
+// LDS permutes.  Every helper below must be called by the whole wave.
+//   row_shr:n  0x110 + n   lane i of each row reads lane i - n of that row
+//                          (lanes i < n read the identity)
+//   row_bcast:15  0x142    rows 1..3 read lane 15 of the previous row
+//   row_bcast:31  0x143    rows 2, 3 read lane 31
+// An inclusive scan is the four in-row shifts and the two broadcasts (rows 1
+// and 3 take row 0's and row 2's total, then rows 2 and 3 take lanes 0..31's).
+template <typename F>
+__device__ inline int wave_incl_scan_op(int x, int ident, F op) {
+  x = op(x, __builtin_amdgcn_update_dpp(ident, x, 0x111, 0xf, 0xf, false));
+  x = op(x, __builtin_amdgcn_update_dpp(ident, x, 0x112, 0xf, 0xf, false));
+  x = op(x, __builtin_amdgcn_update_dpp(ident, x, 0x114, 0xf, 0xf, false));
+  x = op(x, __builtin_amdgcn_update_dpp(ident, x, 0x118, 0xf, 0xf, false));
+  x = op(x, __builtin_amdgcn_update_dpp(ident, x, 0x142, 0xa, 0xf, false));
+  x = op(x, __builtin_amdgcn_update_dpp(ident, x, 0x143, 0xc, 0xf, false));
+  return x;
 }
-__device__ inline int wave_sum(int v) {
-#pragma unroll
-  for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
-  return v;
+__device__ inline int wave_incl_scan(int v) {
+  return wave_incl_scan_op(v, 0, [](int a, int b) { return a + b; });
+}
+__device__ inline int wave_incl_max(int v) {
+  return wave_incl_scan_op(v, INT_MIN, [](int a, int b) { return a > b ? a : b; });
+}
+// total over the wave, the same (scalar) value in every lane
+__device__ inline int wave_sum(int v) { return __builtin_amdgcn_readlane(wave_incl_scan(v), 63); }
+// v_permlane32_swap_b32 with both operands v leaves {v[l], v[l ^ 32]} in every
+// lane l (in an order that depends on the half), so symmetric combinations of a
+// lane and its partner in the other half take one exchange
+__device__ inline float half_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
+                                                 __builtin_bit_cast(uint32_t, v), false, false);
+  return __builtin_elementwise_maximum(__builtin_bit_cast(float, (uint32_t)r[0]),
+                                       __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ inline float half_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
+                                                 __builtin_bit_cast(uint32_t, v), false, false);
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+// the value of lane l ^ 32
+__device__ inline uint32_t half_partner(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return __lane_id() < 32 ? (uint32_t)r[1] : (uint32_t)r[0];
 }
 __device__ inline long long wave_sum64(long long v) {
 #pragma unroll

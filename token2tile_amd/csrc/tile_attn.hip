@@ -437,12 +437,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
         __builtin_amdgcn_wave_barrier();
         if (lane == 0 || st < TA_KT) bMark[lane == 0 ? 0 : st] = lane + 1;
         __builtin_amdgcn_wave_barrier();
-        int k = bMark[lane] - 1;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-          const int y = __shfl_up(k, d, 64);
-          if (lane >= d) k = k > y ? k : y;
-        }
+        const int k = wave_incl_max(bMark[lane] - 1);
         const int pos = base + lane;
         const int ck = __shfl(cs, k, 64), rk = __shfl(rw, k, 64);
         sIdx[tile & 1][lane] = pos < kvlen ? rk + pos - ck : 0;
@@ -495,7 +490,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int a = 0; a < 16; a += 2) mr = vmax(mr, vmax(S[kb][a], S[kb][a + 1]));
-      mr = vmax(mr, __shfl_xor(mr, 32, 64));
+      mr = half_max(mr);
       const float mx = mr * c;
       // lazy max: move only when exceeded, then with headroom
       if (__builtin_amdgcn_readfirstlane((int)(__ballot(mx > m) != 0ull))) {
@@ -559,7 +554,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
         tile_step(B0{}, valid, std::true_type{});
     }
   }
-  const float lt = lsum + __shfl_xor(lsum, 32, 64);
+  const float lt = half_sum(lsum);
   const float inv = kvlen > 0 ? 1.0f / lt : 0.f;
   const float lse2 = kvlen > 0 ? m + __log2f(lt) : -__builtin_inff();
   // exact output of the lane's 64 dims, rounded to T as the exact buffer
@@ -716,7 +711,7 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
       }
     }
     float mx = vmax((float)mp[0], (float)mp[1]);
-    mx = vmax(mx, __shfl_xor(mx, 32, 64));
+    mx = half_max(mx);
     if (__builtin_amdgcn_readfirstlane((int)(__ballot(mx > m2) != 0ull))) {
       T2T_REAL_BRANCH();
       const float mnew = mx > m2 ? mx + TL_MARGIN : m2;
@@ -763,7 +758,7 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
   }
   if (!ok) return;
   // ---- merge under one softmax
-  phi += __shfl_xor(phi, 32, 64);
+  phi = half_sum(phi);
   const float tw = *tailw;
   const float lm = lam[h];
   const float le = lse2v[(size_t)h * N + row] * 0.6931471805599453f;
