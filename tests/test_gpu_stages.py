@@ -132,7 +132,10 @@ def test_select_union_bit_exact(dev, kind, ns):
     assert np.array_equal(c(ub).astype(bool), O.unpack_bits(eu))
 
 
-FUSED_CASES = ["normal", "tied_centroids", "zeros", "one_per_cluster"]
+# alternating_scale: consecutive rows (in the order the kernels walk them)
+# differ in score scale by 2500x, so the lower bound carried over from the
+# previous row is far off and the selection must fall back to a full pass
+FUSED_CASES = ["normal", "tied_centroids", "zeros", "one_per_cluster", "alternating_scale"]
 
 
 @pytest.mark.parametrize("kind", FUSED_CASES)
@@ -160,6 +163,10 @@ def test_score_select_fused_matches_split(dev, kind, ns):
     else:
         qlab = rng.integers(0, CQ - 1, (H, N)).astype(np.int32)   # cluster CQ-1 stays empty
     qperm, qcounts = O.stable_perm(qlab, CQ)
+    if kind == "alternating_scale":
+        scale = np.where(np.arange(N) % 2 == 1, 50.0, 0.02).astype(np.float32)
+        for h in range(H):
+            QU[h, qperm[h]] = (QU[h, qperm[h]].astype(np.float32) * scale[:, None]).astype(np.float16)
     _, cks = ops.centroid_finalize(g(ck2, dev))
     ns_t = torch.tensor(ns, dtype=torch.int32, device=dev)
     gl = ops.score(g(QU, dev), cks)

@@ -6,7 +6,9 @@
 // g < 4, j < 8), and the budget threshold is found exactly with two 8-bit
 // radix passes over a wave-private, size-weighted LDS histogram:
 //   pass 1: high byte of the ordered key, pass 2: low byte inside the
-//   crossing high-byte bin.
+//   crossing high-byte bin.  Only keys above a lower bound carried over from
+//   the previous row enter the histogram (exact: a row whose bounded keys do
+//   not reach the budget is redone without the bound).
 // Ties at the threshold are resolved in ascending cluster order with wave
 // prefix sums.  Each lane keeps the OR of its 32 selection bits across the
 // rows of one query cluster and flushes them with one atomicOr per word when
@@ -17,6 +19,10 @@
 #define SEL_NC 2048
 #define SEL_WAVES 4
 #define SEL_ROWS_PER_WAVE 16
+// per-wave histogram: 256 bins plus one private dump slot per lane, so both
+// passes add every key without a branch (pass 2 sends keys outside the
+// crossing high-byte bin to the lane's own slot: no conflicts, never read)
+#define SEL_HIST (256 + 64)
 
 __device__ inline void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -52,8 +58,11 @@ __global__ __launch_bounds__(1024) void select_prep_kernel(const int32_t* __rest
 
 // Find the bin where the running (descending) weight first reaches ns.
 // hist has 256 bins, bin 255 = largest keys.  Lane l scans bins 255-4l..252-4l.
-// Returns the bin; *above = weight of all higher bins; *inbin = its weight.
-__device__ inline int find_cross(const int* hist, int base, int ns, int* above, int* inbin) {
+// Returns the bin; *above = weight of all higher bins; *inbin = its weight;
+// *total = base + the weight of all bins (below ns: no bin crosses and the
+// returned bin is meaningless).
+__device__ inline int find_cross(const int* hist, int base, int ns, int* above, int* inbin,
+                                 int* total) {
   const int l = __lane_id();
   int w[4];
   int s = 0;
@@ -64,6 +73,7 @@ __device__ inline int find_cross(const int* hist, int base, int ns, int* above, 
   }
   const int inc = wave_incl_scan(s);
   const int ex = inc - s + base;
+  *total = base + __builtin_amdgcn_readlane(inc, 63);
   const bool mine = (ex < ns) && (ex + s >= ns);
   int bin = 0, ab = 0, ib = 0;
   if (mine) {
@@ -88,21 +98,37 @@ __device__ inline int find_cross(const int* hist, int base, int ns, int* above, 
 }
 
 // Selection of one row.  keys/sz: the lane's 32 clusters (index 8 g + j).
-// Returns the lane's 32 selection bits; *rowcnt = selected keys (all lanes).
+// Returns the lane's 32 selection bits; *rowcnt = selected keys (all lanes);
+// *vstar_out = the row's crossing key.
+//
+// lo (wave-uniform) is a guess for a lower bound of the crossing key: the
+// previous row's crossing key minus SEL_BOUND_MARGIN, or SEL_NO_BOUND.  Keys
+// below it go to the lane's private dump slot instead of a histogram bin,
+// which removes the bulk of a row's keys (similar scores share a few high-byte
+// bins) from the same-address atomic conflicts.  The result is exact whenever
+// the clusters with keys >= lo hold >= ns keys: the crossing key is then >= lo
+// and every key at or above it is counted.  Otherwise the row is redone
+// without the bound.
+#define SEL_NO_BOUND (-65536)
+#define SEL_BOUND_MARGIN 1024  // one binade of fp16 keys
 __device__ inline uint32_t select_row(const int (&key)[32], const int (&sz)[32], int* hist, int ns,
-                                      int* rowcnt) {
+                                      int lo, int* rowcnt, int* vstar_out) {
   const int l = __lane_id();
   // ---- pass 1: high byte ----
+  int hb, above1, inbin1, tot1;
+  for (;;) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) hist[4 * l + i] = 0;
-  wave_sync();
+    for (int i = 0; i < 4; ++i) hist[4 * l + i] = 0;
+    wave_sync();
 #pragma unroll
-  for (int i = 0; i < 32; ++i)
-    if (sz[i]) atomicAdd(&hist[(key[i] >> 8) + 128], sz[i]);
-  wave_sync();
-  int above1, inbin1;
-  const int hb = find_cross(hist, 0, ns, &above1, &inbin1);
-  wave_sync();
+    for (int i = 0; i < 32; ++i)  // empty clusters add 0
+      atomicAdd(&hist[key[i] >= lo ? (key[i] >> 8) + 128 : 256 + l], sz[i]);
+    wave_sync();
+    hb = find_cross(hist, 0, ns, &above1, &inbin1, &tot1);
+    wave_sync();
+    if (tot1 >= ns || lo == SEL_NO_BOUND) break;  // wave-uniform
+    lo = SEL_NO_BOUND;
+  }
   // ---- pass 2: low byte within the crossing high-byte bin ----
 #pragma unroll
   for (int i = 0; i < 4; ++i) hist[4 * l + i] = 0;
@@ -110,12 +136,14 @@ __device__ inline uint32_t select_row(const int (&key)[32], const int (&sz)[32],
   const int hsel = hb - 128;
 #pragma unroll
   for (int i = 0; i < 32; ++i)
-    if (sz[i] && (key[i] >> 8) == hsel) atomicAdd(&hist[key[i] & 255], sz[i]);
+    atomicAdd(&hist[(key[i] >> 8) == hsel && key[i] >= lo ? (key[i] & 255) : 256 + l], sz[i]);
   wave_sync();
   int wgt, weq;
-  const int lb = find_cross(hist, above1, ns, &wgt, &weq);
+  int tot2;
+  const int lb = find_cross(hist, above1, ns, &wgt, &weq, &tot2);
   wave_sync();
   const int vstar = hsel * 256 + lb;
+  *vstar_out = vstar;
   // ---- ties at the threshold, in ascending cluster order ----
   int ntie = 0;
 #pragma unroll
@@ -176,7 +204,7 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
     const int32_t* __restrict__ qperm, const int32_t* __restrict__ off,
     const int32_t* __restrict__ ns_dev, int32_t* __restrict__ unip, int32_t* __restrict__ rowcnt,
     int N, int CQ) {
-  __shared__ int hist_all[SEL_WAVES][256];
+  __shared__ int hist_all[SEL_WAVES][SEL_HIST];
   const int h = blockIdx.y;
   const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
   int* hist = hist_all[wv];
@@ -213,6 +241,7 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
   while (t < CQ - 1 && offh[t + 1] <= j0) ++t;  // skip empty clusters
   int tend = offh[t + 1];
   uint32_t acc = 0;
+  int klo = SEL_NO_BOUND, vstar = 0;  // lower-bound guess from the previous row
   const uint16_t* glh = gl + (size_t)h * N * SEL_NC;
   const int32_t* qp = qperm + (size_t)h * N;
   int32_t* uh = unip + (size_t)h * CQ * (SEL_NC / 32);
@@ -238,7 +267,8 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
       }
     }
     int rc;
-    acc |= select_row(key, sz, hist, ns, &rc);
+    acc |= select_row(key, sz, hist, ns, klo, &rc, &vstar);
+    klo = vstar - SEL_BOUND_MARGIN;
     if (l == 0) rowcnt[(size_t)h * N + orig] = rc;
   }
   flush_union(acc, uh + (size_t)t * (SEL_NC / 32));
@@ -263,7 +293,7 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
     const int32_t* __restrict__ off, const int32_t* __restrict__ ns_dev,
     int32_t* __restrict__ unip, int32_t* __restrict__ rowcnt, int N, int CQ) {
   __shared__ __attribute__((aligned(16))) uint16_t sKey[SF_ROWS * SF_PITCH];
-  __shared__ int hist_all[SF_WAVES][256];
+  __shared__ int hist_all[SF_WAVES][SEL_HIST];
   const int h = blockIdx.y;
   const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int jl = l & 31, hh = l >> 5;
@@ -305,6 +335,7 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
   int32_t* uh = unip + (size_t)h * CQ * (SEL_NC / 32);
   int t = -1, tend = 0;
   uint32_t acc = 0;
+  int klo = SEL_NO_BOUND, vstar = 0;  // lower-bound guess from the previous row
   for (int b = 0; b < SF_BATCHES; ++b) {
     const int j0 = base + SF_ROWS * b;
     if (j0 >= lim) break;
@@ -367,7 +398,8 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
         }
       }
       int rc;
-      acc |= select_row(key, sz, hist, ns, &rc);
+      acc |= select_row(key, sz, hist, ns, klo, &rc, &vstar);
+      klo = vstar - SEL_BOUND_MARGIN;
       if (l == 0) rowcnt[(size_t)h * N + qp[j]] = rc;
     }
     __syncthreads();  // the next batch overwrites the keys
