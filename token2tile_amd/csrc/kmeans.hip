@@ -316,7 +316,8 @@ __global__ __launch_bounds__(256) void key_gather_kernel(
     const uint16_t* __restrict__ KU, const uint16_t* __restrict__ V,
     const int32_t* __restrict__ perm, const int32_t* __restrict__ counts,
     const int32_t* __restrict__ cbase, const uint16_t* __restrict__ ck0, float* __restrict__ ck2,
-    uint16_t* __restrict__ V_sorted, float* __restrict__ vsum, int N, int C) {
+    uint16_t* __restrict__ V_sorted, float* __restrict__ vsum, float* __restrict__ cmax, int N,
+    int C) {
   const int h = blockIdx.y;
   const int l = threadIdx.x & 63;
   const int c = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -351,22 +352,29 @@ __global__ __launch_bounds__(256) void key_gather_kernel(
   float* vo = vsum + ((size_t)h * C + c) * 128 + 2 * l;
   vo[0] = v0;
   vo[1] = v1;
+  // the cluster's largest |value sum|, for the per-head scale lam
+  const float mx = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+  if (l == 0) cmax[(size_t)h * C + c] = mx;
   if (ck2 && l < 32) {
     const size_t o = ((size_t)h * C + c) * KM_R + l;
     ck2[o] = n ? ax / (float)n : h2f(ck0[o]);
   }
 }
 
-// lam = max(1, max|vsum| / 32768); sumv = fp16(vsum * (1 / lam)); one block/head
+// lam = max(1, max|vsum| / 32768); sumv = fp16(vsum * (1 / lam)).  The grid
+// spans every head's 128 C values (VS_PER per thread): each block reduces the
+// head's C per-cluster maxima (cmax, written by key_gather_kernel) to lam
+// itself, so the head needs no single-block pass over all of vsum.
+#define VS_PER 8
 __global__ __launch_bounds__(1024) void vstats_kernel(const float* __restrict__ vsum,
+                                                      const float* __restrict__ cmax,
                                                       uint16_t* __restrict__ sumv,
                                                       float* __restrict__ lam, int C) {
   __shared__ float red[16];
-  const int h = blockIdx.x, tid = threadIdx.x;
-  const size_t CE = (size_t)C * 128;
-  const float* vh = vsum + (size_t)h * CE;
+  const int h = blockIdx.y, tid = threadIdx.x;
+  const float* ch = cmax + (size_t)h * C;
   float mx = 0.f;
-  for (size_t i = tid; i < CE; i += 1024) mx = fmaxf(mx, fabsf(vh[i]));
+  for (int i = tid; i < C; i += 1024) mx = fmaxf(mx, ch[i]);
   mx = wave_max(mx);
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
@@ -374,9 +382,19 @@ __global__ __launch_bounds__(1024) void vstats_kernel(const float* __restrict__ 
   for (int i = 0; i < 16; ++i) mx = fmaxf(mx, red[i]);
   const float lm = fmaxf(1.0f, mx / 32768.0f);
   const float inv = 1.0f / lm;
-  if (tid == 0) lam[h] = lm;
+  if (blockIdx.x == 0 && tid == 0) lam[h] = lm;
+  const size_t CE = (size_t)C * 128;
+  const size_t i0 = ((size_t)blockIdx.x * 1024 + tid) * VS_PER;
+  const float* vh = vsum + (size_t)h * CE;
   uint16_t* sh = sumv + (size_t)h * CE;
-  for (size_t i = tid; i < CE; i += 1024) sh[i] = f2h(opaque(vh[i] * inv));
+#pragma unroll
+  for (int e = 0; e < VS_PER; ++e)
+    if (i0 + e < CE) sh[i0 + e] = f2h(opaque(vh[i0 + e] * inv));
+}
+static void launch_vstats(const float* vsum, const float* cmax, void* sumv, float* lam, int H,
+                          int C, hipStream_t st) {
+  hipLaunchKernelGGL(vstats_kernel, dim3(cdiv(C * 128, 1024 * VS_PER), H), dim3(1024), 0, st,
+                     vsum, cmax, (uint16_t*)sumv, lam, C);
 }
 
 // ---------------------------------------------------------------------------
@@ -392,6 +410,7 @@ struct KmmWs {
   int32_t* cbasek;
   int32_t* chist;
   float* vsum;
+  float* cmax;
   size_t total;
 };
 
@@ -409,6 +428,7 @@ static KmmWs kmm_layout(int H, int N, int CQ, int CK, void* base) {
   k.cbasek = w.take<int32_t>((size_t)H * CK);
   k.chist = w.take<int32_t>((size_t)H * nChunk * Cmax);
   k.vsum = w.take<float>((size_t)H * CK * 128);
+  k.cmax = w.take<float>((size_t)H * CK);
   k.total = w.off;
   return k;
 }
@@ -427,11 +447,11 @@ static int launch_assign_km(const void* X, const void* cen, int32_t* lab, int H,
 template <typename T>
 static void launch_key_gather(const void* KU, const void* V, const int32_t* perm,
                               const int32_t* counts, const int32_t* cbase, const void* ck0,
-                              float* ck2, void* V_sorted, float* vsum, int H, int N, int C,
-                              hipStream_t st) {
+                              float* ck2, void* V_sorted, float* vsum, float* cmax, int H, int N,
+                              int C, hipStream_t st) {
   hipLaunchKernelGGL(key_gather_kernel<T>, dim3(cdiv(C, 4), H), dim3(256), 0, st,
                      (const uint16_t*)KU, (const uint16_t*)V, perm, counts, cbase,
-                     (const uint16_t*)ck0, ck2, (uint16_t*)V_sorted, vsum, N, C);
+                     (const uint16_t*)ck0, ck2, (uint16_t*)V_sorted, vsum, cmax, N, C);
 }
 
 #define KM_CHECK(x)            \
@@ -481,13 +501,13 @@ extern "C" int t2t_kmm_run(const void* QU, const void* KU, const void* V, int v_
                             CK - 1, st));
   KM_CHECK(run_sort(klab, kcounts, w.cbasek, kperm, w.chist, H, N, CK, st));
   if (v_dtype == T2T_F16)
-    launch_key_gather<F16T>(KU, V, kperm, kcounts, w.cbasek, ck0, ck2, V_sorted, w.vsum, H, N, CK,
+    launch_key_gather<F16T>(KU, V, kperm, kcounts, w.cbasek, ck0, ck2, V_sorted, w.vsum, w.cmax, H, N, CK,
                             st);
   else
-    launch_key_gather<BF16T>(KU, V, kperm, kcounts, w.cbasek, ck0, ck2, V_sorted, w.vsum, H, N, CK,
+    launch_key_gather<BF16T>(KU, V, kperm, kcounts, w.cbasek, ck0, ck2, V_sorted, w.vsum, w.cmax, H, N, CK,
                              st);
   T2T_LAUNCH_CHECK("key gather");
-  hipLaunchKernelGGL(vstats_kernel, dim3(H), dim3(1024), 0, st, w.vsum, (uint16_t*)sumv, lam, CK);
+  launch_vstats(w.vsum, w.cmax, sumv, lam, H, CK, st);
   T2T_LAUNCH_CHECK("vstats");
   return T2T_OK;
 }
@@ -520,6 +540,7 @@ __global__ __launch_bounds__(1024) void cbase_kernel(const int32_t* __restrict__
 struct VWs {
   int32_t* cbase;
   float* vsum;
+  float* cmax;
   size_t total;
 };
 static VWs vws_layout(int H, int CK, void* base) {
@@ -527,6 +548,7 @@ static VWs vws_layout(int H, int CK, void* base) {
   VWs v;
   v.cbase = w.take<int32_t>((size_t)H * CK);
   v.vsum = w.take<float>((size_t)H * CK * 128);
+  v.cmax = w.take<float>((size_t)H * CK);
   v.total = w.off;
   return v;
 }
@@ -551,11 +573,11 @@ static int vstats_common(const void* V, int v_dtype, const int32_t* kperm, const
   hipLaunchKernelGGL(cbase_kernel, dim3(H), dim3(1024), 0, st, kcounts, w.cbase, CK);
   if (v_dtype == T2T_F16)
     launch_key_gather<F16T>(nullptr, V, kperm, kcounts, w.cbase, nullptr, nullptr, V_sorted,
-                            w.vsum, H, N, CK, st);
+                            w.vsum, w.cmax, H, N, CK, st);
   else
     launch_key_gather<BF16T>(nullptr, V, kperm, kcounts, w.cbase, nullptr, nullptr, V_sorted,
-                             w.vsum, H, N, CK, st);
-  hipLaunchKernelGGL(vstats_kernel, dim3(H), dim3(1024), 0, st, w.vsum, (uint16_t*)sumv, lam, CK);
+                             w.vsum, w.cmax, H, N, CK, st);
+  launch_vstats(w.vsum, w.cmax, sumv, lam, H, CK, st);
   T2T_LAUNCH_CHECK("vstats");
   return T2T_OK;
 }
