@@ -310,7 +310,7 @@ __global__ __launch_bounds__(256) void fixed_mean_kernel(const uint16_t* __restr
 // each) and V (two dims per lane) in sorted row order; V_sorted rows; ck2.
 // perm == nullptr: rows are already cluster ordered (V_sorted input).
 // ---------------------------------------------------------------------------
-#define KG_UNR 8
+#define KG_UNR 16
 template <typename T>
 __global__ __launch_bounds__(256) void key_gather_kernel(
     const uint16_t* __restrict__ KU, const uint16_t* __restrict__ V,
