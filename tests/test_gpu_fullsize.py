@@ -19,7 +19,8 @@ from oracle import t2t_oracle as O
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = ["wan480p", "wan720p", "h3", "h3_5pct"]
+SHAPES = [("wan480p", torch.bfloat16), ("wan720p", torch.bfloat16), ("h3", torch.bfloat16),
+          ("h3_5pct", torch.bfloat16), ("wan480p", torch.float16)]
 
 
 def cos(a, b):
@@ -28,13 +29,13 @@ def cos(a, b):
     return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-30))
 
 
-@pytest.mark.parametrize("name", SHAPES)
-def test_full_size_call(dev, name):
+@pytest.mark.parametrize("name,dtype", SHAPES, ids=[f"{n}-{str(d)[6:]}" for n, d in SHAPES])
+def test_full_size_call(dev, name, dtype):
     from token2tile_amd import ops, synth
     from token2tile_amd.deploy_step import MaskedStepDeploy
     H, N, grid, frac, CQ = synth.CONFIGS[name]
-    print(f"[fullsize] {name}: H={H} N={N} CQ={CQ} frac={frac}", flush=True)
-    q, k, v = synth.generate(H, N, grid=grid, seed=11, device=dev, dtype=torch.bfloat16)
+    print(f"[fullsize] {name} {dtype}: H={H} N={N} CQ={CQ} frac={frac}", flush=True)
+    q, k, v = synth.generate(H, N, grid=grid, seed=11, device=dev, dtype=dtype)
     op = MaskedStepDeploy(H, N, CQ, s_frac=frac, device=dev)
     state = op.init_state(q, k, seed=3)
     st0 = {n_: t_.clone() for n_, t_ in state.items()}
