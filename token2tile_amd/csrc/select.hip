@@ -61,21 +61,26 @@ __global__ __launch_bounds__(1024) void select_prep_kernel(const int32_t* __rest
 // Returns the bin; *above = weight of all higher bins; *inbin = its weight;
 // *total = base + the weight of all bins (below ns: no bin crosses and the
 // returned bin is meaningless).
+// PACKED: the bins hold (weight << 12) | key count; *count = the crossing
+// bin's key count (unused otherwise).
+template <bool PACKED = false>
 __device__ inline int find_cross(const int* hist, int base, int ns, int* above, int* inbin,
-                                 int* total) {
+                                 int* total, int* count = nullptr) {
   const int l = __lane_id();
-  int w[4];
+  int w[4], cn[4];
   int s = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    w[i] = hist[255 - 4 * l - i];
+    const int raw = hist[255 - 4 * l - i];
+    w[i] = PACKED ? raw >> 12 : raw;
+    cn[i] = raw & 0xfff;
     s += w[i];
   }
   const int inc = wave_incl_scan(s);
   const int ex = inc - s + base;
   *total = base + __builtin_amdgcn_readlane(inc, 63);
   const bool mine = (ex < ns) && (ex + s >= ns);
-  int bin = 0, ab = 0, ib = 0;
+  int bin = 0, ab = 0, ib = 0, ic = 0;
   if (mine) {
     int cum = ex;
     bool done = false;
@@ -85,6 +90,7 @@ __device__ inline int find_cross(const int* hist, int base, int ns, int* above, 
         bin = 255 - 4 * l - i;
         ab = cum;
         ib = w[i];
+        ic = cn[i];
         done = true;
       }
       cum += w[i];
@@ -94,6 +100,7 @@ __device__ inline int find_cross(const int* hist, int base, int ns, int* above, 
   const int src = bal ? (int)__ffsll((long long)bal) - 1 : 0;
   *above = __builtin_amdgcn_readlane(ab, src);
   *inbin = __builtin_amdgcn_readlane(ib, src);
+  if (PACKED) *count = __builtin_amdgcn_readlane(ic, src);
   return __builtin_amdgcn_readlane(bin, src);
 }
 
@@ -136,23 +143,26 @@ __device__ inline uint32_t select_row(const int (&key)[32], const int (&sz)[32],
   const int hsel = hb - 128;
 #pragma unroll
   for (int i = 0; i < 32; ++i)
-    atomicAdd(&hist[(key[i] >> 8) == hsel && key[i] >= lo ? (key[i] & 255) : 256 + l], sz[i]);
+    atomicAdd(&hist[(key[i] >> 8) == hsel && key[i] >= lo ? (key[i] & 255) : 256 + l],
+              (sz[i] << 12) | 1);  // weight and key count (weights < 2^19, counts < 2^12)
   wave_sync();
-  int wgt, weq;
-  int tot2;
-  const int lb = find_cross(hist, above1, ns, &wgt, &weq, &tot2);
+  int wgt, weq, tot2, ntie;
+  const int lb = find_cross<true>(hist, above1, ns, &wgt, &weq, &tot2, &ntie);
   wave_sync();
   const int vstar = hsel * 256 + lb;
   *vstar_out = vstar;
-  // ---- ties at the threshold, in ascending cluster order ----
-  int ntie = 0;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) ntie += (key[i] == vstar);
-  ntie = wave_sum(ntie);
+  // ---- ties at the threshold (ntie clusters hold the key vstar), in
+  //      ascending cluster order ----
   uint32_t bits = 0;
   if (ntie == 1) {
+    // bit i = key[i] >= vstar, shifted in from bit 31 down: compare into VCC,
+    // then bits = bits + bits + carry (two instructions per key)
 #pragma unroll
-    for (int i = 0; i < 32; ++i) bits |= (uint32_t)(key[i] >= vstar) << i;
+    for (int i = 31; i >= 0; --i)
+      asm("v_cmp_ge_i32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
+          : "+v"(bits)
+          : "v"(key[i]), "v"(vstar)
+          : "vcc");
     *rowcnt = wgt + weq;
     return bits;
   }
