@@ -291,10 +291,13 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
 // the instruction, operand split and fp16 rounding of score_kernel (so the
 // scores, and the selection, are bit-identical to the unfused path), and
 // stores the ordered keys in LDS; then every wave selects 4 of the rows.
+// A work-group walks 16 batches (512 rows): the centroid fragments and
+// cluster sizes it loads once are amortised over them, and the next batch's
+// query rows load while the current batch is being selected.
 // ---------------------------------------------------------------------------
 #define SF_WAVES 8
 #define SF_ROWS 32
-#define SF_BATCHES 4
+#define SF_BATCHES 16
 #define SF_PITCH (SEL_NC + 8)  // halves per LDS key row (16-byte aligned rows)
 
 __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
@@ -346,17 +349,24 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
   int t = -1, tend = 0;
   uint32_t acc = 0;
   int klo = SEL_NO_BOUND, vstar = 0;  // lower-bound guess from the previous row
+  // projected query rows of a batch (the B operands): lane jl's row, dims
+  // 8 hh .. and 16 + 8 hh ..
+  auto load_rows = [&](int j0, u32x4& b0, u32x4& b1) {
+    const int row = j0 + jl;
+    b0 = u32x4{0u, 0u, 0u, 0u};
+    b1 = u32x4{0u, 0u, 0u, 0u};
+    if (row < lim) {
+      const uint16_t* qr = qh + (size_t)qp[row] * 32 + 8 * hh;
+      b0 = *(const u32x4*)(qr);
+      b1 = *(const u32x4*)(qr + 16);
+    }
+  };
+  u32x4 b0, b1;
+  load_rows(base, b0, b1);
   for (int b = 0; b < SF_BATCHES; ++b) {
     const int j0 = base + SF_ROWS * b;
     if (j0 >= lim) break;
     {  // scores of rows j0 .. j0 + 31 against the wave's centroids -> keys in LDS
-      const int row = j0 + jl;
-      u32x4 b0 = {0u, 0u, 0u, 0u}, b1 = {0u, 0u, 0u, 0u};
-      if (row < lim) {
-        const uint16_t* qr = qh + (size_t)qp[row] * 32 + 8 * hh;
-        b0 = *(const u32x4*)(qr);
-        b1 = *(const u32x4*)(qr + 16);
-      }
       uint16_t* krow = sKey + jl * SF_PITCH + 256 * wv + 4 * hh;
 #pragma unroll
       for (int cb = 0; cb < 8; ++cb) {
@@ -376,6 +386,8 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
         }
       }
     }
+    // the next batch's rows load while this batch is selected
+    load_rows(j0 + SF_ROWS, b0, b1);
     __syncthreads();
 #pragma unroll 1
     for (int i = 0; i < SF_ROWS / SF_WAVES; ++i) {
