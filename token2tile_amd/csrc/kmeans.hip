@@ -27,6 +27,8 @@ static inline int pad32(int c) { return (c + 31) & ~31; }
 template <int MODE, int D>
 __global__ __launch_bounds__(256) void assign_kernel(const uint16_t* __restrict__ X,
                                                      const uint16_t* __restrict__ cen,
+                                                     const uint16_t* __restrict__ cprep,
+                                                     const float* __restrict__ cnorm,
                                                      int32_t* __restrict__ labels, int N, int C,
                                                      int pin_begin, int pin_label, int ibits) {
   constexpr int KS = D / 16;
@@ -62,7 +64,23 @@ __global__ __launch_bounds__(256) void assign_kernel(const uint16_t* __restrict_
   for (int c0 = 0; c0 < Cp; c0 += AS_CHUNK) {
     const int nc = (Cp - c0) < AS_CHUNK ? (Cp - c0) : AS_CHUNK;
     __syncthreads();
-    // stage the chunk: -2c (MODE 0, exact in fp16) or c (MODE 1); padding = 0
+    // stage the chunk: -2c (MODE 0, exact in fp16) or c (MODE 1); padding = 0.
+    // With cprep (MODE 0) the negated centroids and their norms come from
+    // cen_prep_kernel, computed once per launch instead of once per block.
+    if (cprep) {
+      const uint16_t* cph = cprep + (size_t)h * C * D;
+      for (int i = tid; i < nc * D / 8; i += 256) {
+        const int ci = c0 + (i * 8) / D;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (ci < C) v = ((const u32x4*)(cph + (size_t)c0 * D))[i];
+        ((u32x4*)sC)[i] = v;
+      }
+      for (int i = tid; i < nc; i += 256) {
+        const int ci = c0 + i;
+        sN[i] = (ci < C) ? cnorm[(size_t)h * C + ci] : __builtin_inff();
+      }
+      __syncthreads();
+    } else {
     for (int i = tid; i < nc * D / 8; i += 256) {
       const int ci = c0 + (i * 8) / D;
       u32x4 v = {0u, 0u, 0u, 0u};
@@ -89,6 +107,7 @@ __global__ __launch_bounds__(256) void assign_kernel(const uint16_t* __restrict_
       sN[i] = (ci < C) ? s : __builtin_inff();
     }
     __syncthreads();
+    }
     for (int cb = 0; cb < nc / 32; ++cb) {
       f32x16 acc;
 #pragma unroll
@@ -411,6 +430,8 @@ struct KmmWs {
   int32_t* chist;
   float* vsum;
   float* cmax;
+  uint16_t* cprep;  // -2c of the centroids of the assignment in flight
+  float* cnorm;     // and their squared norms
   size_t total;
 };
 
@@ -429,6 +450,8 @@ static KmmWs kmm_layout(int H, int N, int CQ, int CK, void* base) {
   k.chist = w.take<int32_t>((size_t)H * nChunk * Cmax);
   k.vsum = w.take<float>((size_t)H * CK * 128);
   k.cmax = w.take<float>((size_t)H * CK);
+  k.cprep = w.take<uint16_t>((size_t)H * Cmax * KM_R);
+  k.cnorm = w.take<float>((size_t)H * Cmax);
   k.total = w.off;
   return k;
 }
@@ -437,10 +460,33 @@ extern "C" size_t t2t_kmm_ws_bytes(int H, int N, int CQ, int CK) {
   return kmm_layout(H, N, CQ, CK, nullptr).total;
 }
 
+// -2c (exact in fp16) and the fp32 squared norm of every centroid, summed
+// sequentially over the dims (each square is exact), as assign_kernel's
+// MODE 0 staging computes them
+__global__ __launch_bounds__(256) void cen_prep_kernel(const uint16_t* __restrict__ cen,
+                                                       uint16_t* __restrict__ cprep,
+                                                       float* __restrict__ cnorm, int C) {
+  const int h = blockIdx.y, ci = blockIdx.x * 256 + threadIdx.x;
+  if (ci >= C) return;
+  const uint16_t* cp = cen + ((size_t)h * C + ci) * KM_R;
+  uint16_t* op = cprep + ((size_t)h * C + ci) * KM_R;
+  float s = 0.f;
+  for (int d = 0; d < KM_R; ++d) {
+    const float v = h2f(cp[d]);
+    s = s + v * v;
+    op[d] = f2h(-2.0f * v);
+  }
+  cnorm[(size_t)h * C + ci] = s;
+}
+
 static int launch_assign_km(const void* X, const void* cen, int32_t* lab, int H, int N, int C,
-                            int pin_begin, int pin_label, hipStream_t st) {
+                            int pin_begin, int pin_label, uint16_t* cprep, float* cnorm,
+                            hipStream_t st) {
+  hipLaunchKernelGGL(cen_prep_kernel, dim3(cdiv(C, 256), H), dim3(256), 0, st,
+                     (const uint16_t*)cen, cprep, cnorm, C);
   hipLaunchKernelGGL((assign_kernel<0, KM_R>), dim3(cdiv(N, 128), H), dim3(256), 0, st,
-                     (const uint16_t*)X, (const uint16_t*)cen, lab, N, C, pin_begin, pin_label, 0);
+                     (const uint16_t*)X, (const uint16_t*)cen, (const uint16_t*)cprep,
+                     (const float*)cnorm, lab, N, C, pin_begin, pin_label, 0);
   return t2t_check_launch("assign");
 }
 
@@ -483,14 +529,14 @@ extern "C" int t2t_kmm_run(const void* QU, const void* KU, const void* V, int v_
   KmmWs w = kmm_layout(H, N, CQ, CK, ws);
   const int nores = N + 1;  // no pinned rows
   // query pass 1
-  KM_CHECK(launch_assign_km(QU, cq0, w.qlab1, H, N, CQ, nores, 0, st));
+  KM_CHECK(launch_assign_km(QU, cq0, w.qlab1, H, N, CQ, nores, 0, w.cprep, w.cnorm, st));
   KM_CHECK(run_sort(w.qlab1, w.counts1, w.cbase1, w.perm1, w.chist, H, N, CQ, st));
   hipLaunchKernelGGL(fixed_mean_kernel<0>, dim3(cdiv(CQ, 4), H), dim3(256), 0, st,
                      (const uint16_t*)QU, w.perm1, w.counts1, w.cbase1, (const uint16_t*)cq0,
                      w.cq1, N, CQ);
   T2T_LAUNCH_CHECK("qmean 1");
   // query pass 2
-  KM_CHECK(launch_assign_km(QU, w.cq1, qlab, H, N, CQ, nores, 0, st));
+  KM_CHECK(launch_assign_km(QU, w.cq1, qlab, H, N, CQ, nores, 0, w.cprep, w.cnorm, st));
   KM_CHECK(run_sort(qlab, qcounts, w.cbaseq, qperm, w.chist, H, N, CQ, st));
   hipLaunchKernelGGL(fixed_mean_kernel<0>, dim3(cdiv(CQ, 4), H), dim3(256), 0, st,
                      (const uint16_t*)QU, qperm, qcounts, w.cbaseq, (const uint16_t*)w.cq1,
@@ -498,7 +544,7 @@ extern "C" int t2t_kmm_run(const void* QU, const void* KU, const void* V, int v_
   T2T_LAUNCH_CHECK("qmean 2");
   // key pass
   KM_CHECK(launch_assign_km(KU, ck0, klab, H, N, CK, pin_tail > 0 ? N - pin_tail : nores,
-                            CK - 1, st));
+                            CK - 1, w.cprep, w.cnorm, st));
   KM_CHECK(run_sort(klab, kcounts, w.cbasek, kperm, w.chist, H, N, CK, st));
   if (v_dtype == T2T_F16)
     launch_key_gather<F16T>(KU, V, kperm, kcounts, w.cbasek, ck0, ck2, V_sorted, w.vsum, w.cmax, H, N, CK,
@@ -612,13 +658,16 @@ extern "C" int t2t_fast_assign(const void* x, const void* c, int32_t* labels, in
   const dim3 g(cdiv(N, 128), H);
   if (D == 32)
     hipLaunchKernelGGL((assign_kernel<1, 32>), g, dim3(256), 0, st, (const uint16_t*)x,
-                       (const uint16_t*)c, labels, N, C, N + 1, 0, ibits);
+                       (const uint16_t*)c, (const uint16_t*)nullptr, (const float*)nullptr, labels, N, C,
+                       N + 1, 0, ibits);
   else if (D == 64)
     hipLaunchKernelGGL((assign_kernel<1, 64>), g, dim3(256), 0, st, (const uint16_t*)x,
-                       (const uint16_t*)c, labels, N, C, N + 1, 0, ibits);
+                       (const uint16_t*)c, (const uint16_t*)nullptr, (const float*)nullptr, labels, N, C,
+                       N + 1, 0, ibits);
   else
     hipLaunchKernelGGL((assign_kernel<1, 128>), g, dim3(256), 0, st, (const uint16_t*)x,
-                       (const uint16_t*)c, labels, N, C, N + 1, 0, ibits);
+                       (const uint16_t*)c, (const uint16_t*)nullptr, (const float*)nullptr, labels, N, C,
+                       N + 1, 0, ibits);
   T2T_LAUNCH_CHECK("fast_assign");
   return T2T_OK;
 }
