@@ -688,14 +688,14 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
       nw0 = ur[2 * tc + 2];
       nw1 = ur[2 * tc + 3];
     }
-    // fp16 scores of the lane's query against centroids 32 kb + 8 (a / 4) +
-    // 4 hh + a % 4 of the tile, as pairs; centroids in the query's union ->
-    // -inf.  The union bit becomes an all-ones/zero word (opaque to the
-    // compiler, so the select stays one bitfield insert instead of a compare
-    // and a conditional move); the max runs on the packed pairs and the
-    // exponent argument reads the fp16 halves directly (v_fma_mix_f32).
-    f16x2 sp[2][8];
-    f16x2 mp = {(_Float16)-__builtin_inff(), (_Float16)-__builtin_inff()};
+    // per 32-centroid half kb: fp16 scores of the lane's query against
+    // centroids 32 kb + 8 (a / 4) + 4 hh + a % 4, as pairs, with the union's
+    // centroids at -inf (the union bit spread to an all-ones / zero half and
+    // one bitfield insert; the max runs on the packed pairs and the exponent
+    // argument reads the fp16 halves directly, v_fma_mix_f32); then the
+    // running max, the exponentials and P V of the half.  Working a half at a
+    // time keeps the live scores and P fragments small.
+    const uint16_t* vt = sb + 2048;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int r = 32 * kb + jl;
@@ -703,49 +703,49 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
       S = Mfma<F16T>::run(*(const u32x4*)(sb + rc_off(r, hh)), qu0, S);
       S = Mfma<F16T>::run(*(const u32x4*)(sb + rc_off(r, 2 + hh)), qu1, S);
       const uint32_t u = (kb ? uw1 : uw0) >> (4 * hh);  // element a <-> bit 8 (a / 4) + a % 4
+      f16x2 sp[8];
+      f16x2 mp = {(_Float16)-__builtin_inff(), (_Float16)-__builtin_inff()};
 #pragma unroll
       for (int a = 0; a < 16; a += 2) {
         const uint32_t pk = Pk<F16T>::pack(S[a], S[a + 1]);
-        sp[kb][a / 2] = __builtin_bit_cast(f16x2, mask_pair_neg_inf(pk, u, 8 * (a / 4) + (a % 4)));
-        mp = __builtin_elementwise_maximum(mp, sp[kb][a / 2]);
+        sp[a / 2] = __builtin_bit_cast(f16x2, mask_pair_neg_inf(pk, u, 8 * (a / 4) + (a % 4)));
+        mp = __builtin_elementwise_maximum(mp, sp[a / 2]);
       }
-    }
-    float mx = vmax((float)mp[0], (float)mp[1]);
-    mx = half_max(mx);
-    if (__builtin_amdgcn_readfirstlane((int)(__ballot(mx > m2) != 0ull))) {
-      T2T_REAL_BRANCH();
-      const float mnew = mx > m2 ? mx + TL_MARGIN : m2;
-      const float alpha = __builtin_amdgcn_exp2f((m2 - mnew) * L2E);
-      m2 = mnew;
-      phi *= alpha;
+      float mx = vmax((float)mp[0], (float)mp[1]);
+      mx = half_max(mx);
+      if (__builtin_amdgcn_readfirstlane((int)(__ballot(mx > m2) != 0ull))) {
+        T2T_REAL_BRANCH();
+        const float mnew = mx > m2 ? mx + TL_MARGIN : m2;
+        const float alpha = __builtin_amdgcn_exp2f((m2 - mnew) * L2E);
+        m2 = mnew;
+        phi *= alpha;
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
+        for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-        for (int a = 0; a < 16; ++a) O[nb][a] *= alpha;
-    }
-    const float nm = -m2 * L2E;
-    u32x4 pb[4];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+          for (int a = 0; a < 16; ++a) O[nb][a] *= alpha;
+      }
+      const float nm = -m2 * L2E;
+      u32x4 pb[2];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const f32x4 cn = *(const f32x4*)(sCnt + TL_CT * tc + 32 * kb + 8 * j + 4 * hh);
         float pe[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          pe[e] = __builtin_amdgcn_exp2f(fmaf((float)sp[kb][2 * j + e / 2][e % 2], L2E, nm));
+          pe[e] = __builtin_amdgcn_exp2f(fmaf((float)sp[2 * j + e / 2][e % 2], L2E, nm));
           phi = fmaf(pe[e], cn[e], phi);
         }
-        pb[2 * kb + j / 2][2 * (j % 2)] = Pk<F16T>::pack(pe[0], pe[1]);
-        pb[2 * kb + j / 2][2 * (j % 2) + 1] = Pk<F16T>::pack(pe[2], pe[3]);
+        pb[j / 2][2 * (j % 2)] = Pk<F16T>::pack(pe[0], pe[1]);
+        pb[j / 2][2 * (j % 2) + 1] = Pk<F16T>::pack(pe[2], pe[3]);
       }
-    const uint16_t* vt = sb + 2048;
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      const int dim = 32 * nb + jl;
+      for (int nb = 0; nb < 4; ++nb) {
+        const int dim = 32 * nb + jl;
 #pragma unroll
-      for (int mm = 0; mm < 4; ++mm)
-        O[nb] = Mfma<F16T>::run(*(const u32x4*)(vt + vt_unit_off(dim, 2 * mm + hh)), pb[mm], O[nb]);
+        for (int m = 0; m < 2; ++m)
+          O[nb] = Mfma<F16T>::run(*(const u32x4*)(vt + vt_unit_off(dim, 2 * (2 * kb + m) + hh)), pb[m],
+                                  O[nb]);
+      }
     }
     uw0 = nw0;
     uw1 = nw1;
