@@ -441,8 +441,14 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
         const int pos = base + lane;
         const int ck = __shfl(cs, k, 64), rk = __shfl(rw, k, 64);
         sIdx[tile & 1][lane] = pos < kvlen ? rk + pos - ck : 0;
-        // run holding the next tile's first position
-        r0 += __popcll(__ballot(st <= TA_KT)) - 1;
+        // run holding the next tile's first position: the last run starting at
+        // or before it.  The lanes see runs r0 .. r0 + 63 only; when all of
+        // them qualify (64 runs of one key each), run r0 + 64 may start exactly
+        // there too and is checked separately.
+        const int seen = __popcll(__ballot(st <= TA_KT));
+        int nxt = r0 + seen - 1;
+        if (seen == 64 && r0 + 64 < nrun && run_cum(r0 + 64) <= base + TA_KT) nxt = r0 + 64;
+        r0 = nxt;
       }
     };
     // K and V tiles via LDS DMA (each wave instruction fills 4 whole rows, the

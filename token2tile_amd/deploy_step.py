@@ -305,6 +305,7 @@ class MaskedStepDeploy:
                     ops.project(q, snap["Uq"], out=self.QU, stream=s0)
                 with self._stage("gather_k"):
                     ops.fast_gather(k, snap["kperm"], out=io["kp"], stream=s0)
+                kperm = snap["kperm"]
                 with self._stage("vstats"):
                     ops.vstats_gather(v, snap["kperm"], snap["counts"], V_sorted=io["vp"],
                                       sumv=self._kmm_sumv, lam=self._kmm_lam, ws=self._ws_vst,
@@ -349,6 +350,7 @@ class MaskedStepDeploy:
                         ops.union_or_last(unip, stream=s0)
                 with self._stage("gather_k"):
                     ops.fast_gather(k, km_out["kperm"], out=io["kp"], stream=s0)
+                kperm = km_out["kperm"]
                 plan = (held["tile_attn_plan"] if recycle else
                         torch.empty(self._tile_attn_plan_ints, device=self.dev, dtype=torch.int32))
                 rebuild = True
@@ -386,5 +388,5 @@ class MaskedStepDeploy:
         cur.wait_stream(s0)
         cur.wait_stream(s1)
         self._last = dict(unip=unip, qperm=qperm, tile_sizes=tile_sizes, counts=counts,
-                          qlab=qlab_cur, cks=cks, plan=plan)
+                          qlab=qlab_cur, cks=cks, plan=plan, kperm=kperm)
         return io["out"]
