@@ -119,6 +119,17 @@ def test_bad_inputs_raise(dev):
     bad[0, 5, 5] = float("nan")
     with pytest.raises(RuntimeError):
         deploy.init_state(bad, tq)
+    # fewer tokens than clusters
+    with pytest.raises(ValueError, match="cannot seed"):
+        MaskedStepDeploy(1, 1000, 32, device=dev)
+    # a state of the wrong geometry never reaches the kernels
+    state = deploy.init_state(tq, tq, seed=0)
+    for name, cut in (("ck", 1024), ("cq", 16)):
+        broken = dict(state, **{name: state[name][:, :cut].contiguous()})
+        with pytest.raises(ValueError, match=name):
+            deploy.step(tq, tq, tq, broken)
+    with pytest.raises(ValueError, match="Uq"):
+        deploy.step(tq, tq, tq, dict(state, Uq=state["Uq"].float()))
 
 
 # awkward shapes: N not a multiple of any tile, CQ not a power of two, one key

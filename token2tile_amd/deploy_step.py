@@ -140,6 +140,8 @@ class MaskedStepDeploy:
             raise ValueError("CQ must be in [1, 4096]")
         if N >= 524288:
             raise ValueError("the selection packing requires N < 524288")
+        if N < C or N < CQ:
+            raise ValueError(f"N={N} tokens cannot seed {C} key clusters and {CQ} query clusters")
         self.H, self.N, self.CQ, self.C, self.D, self.r = H, N, CQ, C, D, r
         self.ns = max(1, int(s_frac * N))
         self.tailw = tailw
@@ -278,6 +280,15 @@ class MaskedStepDeploy:
                                  f"{self.dev}")
         if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.float16, torch.bfloat16):
             raise TypeError("step: q, k, v must share dtype fp16 or bf16")
+        # the kernels take raw pointers: a state of the wrong geometry would be
+        # read out of bounds, so it is checked here
+        for name, shape in (("Uq", (H, D, self.r)), ("Uk", (H, D, self.r)), ("ck", (H, C, self.r)),
+                            ("cq", (H, CQ, self.r))):
+            t = state.get(name)
+            if (t is None or tuple(t.shape) != shape or t.dtype != torch.float16
+                    or t.device != self.dev):
+                raise ValueError(f"step: state[{name!r}] must be an fp16 {list(shape)} tensor on "
+                                 f"{self.dev}")
         caller = torch.cuda.current_stream(self.dev)
         s0, s1 = self.s_main, self.s_side
         if caller != s0:
