@@ -413,3 +413,57 @@ def test_fused_attention_tail_matches_oracle(dev, dtype):
     assert np.abs(got - eo).max() < tol
     a, b = got.ravel().astype(np.float64), eo.ravel()
     assert a @ b / (np.linalg.norm(a) * np.linalg.norm(b)) > 0.9999
+
+
+def test_wrappers_reject_mismatched_tensors(dev):
+    """Every wrapper checks each tensor's shape, dtype and device before a
+    kernel sees its pointer; each case below would otherwise be read or written
+    out of bounds.  Nothing here launches a kernel."""
+    from token2tile_amd import ops
+    H, N, CQ = 2, 640, 8
+    z = lambda *s, dt=torch.int32: torch.zeros(*s, dtype=dt, device=dev)  # noqa: E731
+    q = z(H, N, 128, dt=torch.bfloat16)
+    kcounts, qcounts, unip, qperm = z(H, 2048), z(H, CQ), z(H, CQ, 64), z(H, N)
+    QU, cks = z(H, N, 32, dt=torch.float16), z(H, 2048, 32, dt=torch.float16)
+    sumv, lam = z(H, 2048, 128, dt=torch.float16), z(H, dt=torch.float32)
+    tailw = torch.tensor(1.0, device=dev)
+    plan = z(ops.plan_ints(H, N, CQ))
+    ns = z(1)
+    bad = [
+        lambda: ops.fast_gather(q, z(H, N - 1)),
+        lambda: ops.fast_gather(q, qperm.to(torch.int64)),
+        lambda: ops.fast_gather(q, qperm, out=torch.empty_like(q, dtype=torch.float16)),
+        lambda: ops.tile_plan(qcounts, z(H, 1024), unip, N),
+        lambda: ops.tile_plan(qcounts, kcounts, unip, N, plan=plan[:-1]),
+        lambda: ops.tile_attn_exact(q, q[:, :-1].contiguous(), q, kcounts, unip, qperm, plan),
+        lambda: ops.tile_attn_exact(q, q, q.to(torch.float16), kcounts, unip, qperm, plan),
+        lambda: ops.tile_attn_exact(q, q, q, kcounts, unip, qperm.cpu(), plan),
+        lambda: ops.tile_attn_run_planned(q, q, q, qcounts, kcounts, unip, QU, cks, sumv[:, :1024],
+                                          lam, qperm, qperm, tailw, torch.empty_like(q), plan,
+                                          True),
+        lambda: ops.tile_attn_run_planned(q, q, q, qcounts, kcounts, unip, QU, cks, sumv, lam,
+                                          qperm, qperm, tailw.double(), torch.empty_like(q),
+                                          plan, True),
+        lambda: ops.tail_merge(q, z(H, N, dt=torch.float32), QU, cks, sumv, kcounts, unip, qperm,
+                               qperm, z(H + 1, dt=torch.float32), tailw),
+        lambda: ops.centroid_tiles(cks, sumv, tiles=z(16, dt=torch.uint8)),
+        lambda: ops.score_select(QU, cks, kcounts, z(H, N + 1), qcounts, ns),
+        lambda: ops.score_select(QU, cks, kcounts, qperm, qcounts, z(2)),
+        lambda: ops.score_select(QU, cks, kcounts, qperm, qcounts, ns,
+                                 ws=z(1 << 20, dt=torch.float32)),
+        lambda: ops.select_union(z(H, N, 2048, dt=torch.float16), kcounts, qperm, qcounts, ns,
+                                 unip=z(H, CQ, 32)),
+        lambda: ops.vstats(q, z(H, 2048, dt=torch.int64)),
+        lambda: ops.vstats_gather(q, qperm, kcounts, lam=z(H, 2, dt=torch.float32)),
+        lambda: ops.kmm_run(QU, QU, q[:, :-1].contiguous(), z(H, CQ, 32, dt=torch.float16),
+                            cks),
+        lambda: ops.fast_assign_labels(QU, z(H, 16, 16, dt=torch.float16)),
+        lambda: ops.det_centroid_update(QU, z(H, N - 1), z(H, 16, 32, dt=torch.float16)),
+        lambda: ops.project(q.transpose(1, 2), z(H, 128, 32, dt=torch.float16)),
+        lambda: ops.union_or_last(z(H, CQ, 63)),
+    ]
+    for i, f in enumerate(bad):
+        with pytest.raises(ValueError):
+            f()
+            pytest.fail(f"case {i} was accepted")
+    torch.cuda.synchronize()

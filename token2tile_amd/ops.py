@@ -31,18 +31,56 @@ def _ws(nbytes, device):
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
-def _check(t, shape, dtype, name):
-    if tuple(t.shape) != tuple(shape) or t.dtype != dtype or not t.is_contiguous():
-        raise ValueError(f"t2t: {name} must be contiguous {dtype} {tuple(shape)}, "
-                         f"got {t.dtype} {tuple(t.shape)}")
+def _ws_for(ws, nbytes, device):
+    """A caller's workspace if it is a large enough uint8 buffer on ``device``,
+    else a fresh one.  Its byte count is passed to the library, which checks it."""
+    if ws is not None:
+        if (not isinstance(ws, torch.Tensor) or ws.dtype != torch.uint8
+                or not ws.is_contiguous() or ws.device != device):
+            raise ValueError(f"t2t: ws must be a contiguous uint8 tensor on {device}")
+        if ws.numel() >= nbytes:
+            return ws
+    return _ws(nbytes, device)
+
+
+_HALF = (torch.float16, torch.bfloat16)
+
+
+def _check(t, shape, dtype, name, device=None):
+    """The kernels take raw pointers and trust these geometries: a tensor of
+    another shape, dtype or device would be read or written out of bounds."""
+    dtypes = dtype if isinstance(dtype, tuple) else (dtype,)
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"t2t: {name} must be a tensor")
+    if (tuple(t.shape) != tuple(shape) or t.dtype not in dtypes or not t.is_contiguous()
+            or not t.is_cuda or (device is not None and t.device != device)):
+        raise ValueError(f"t2t: {name} must be a contiguous {'/'.join(map(str, dtypes))} "
+                         f"{tuple(shape)} tensor on {device or 'the GPU'}, got {t.dtype} "
+                         f"{tuple(t.shape)} on {t.device}")
+
+
+def _check_ns(ns_t, device):
+    if not isinstance(ns_t, torch.Tensor) or ns_t.numel() != 1 or ns_t.dtype != _i32 \
+            or ns_t.device != device:
+        raise ValueError(f"t2t: ns_t must be a one-element int32 tensor on {device}")
+
+
+def _check_plan(plan, H, N, CQ, device):
+    if (not isinstance(plan, torch.Tensor) or plan.dtype != _i32 or not plan.is_contiguous()
+            or plan.device != device or plan.numel() < plan_ints(H, N, CQ)):
+        raise ValueError(f"t2t: plan must be a contiguous int32 tensor of >= "
+                         f"{plan_ints(H, N, CQ)} elements on {device}")
 
 
 def project(x, U, out=None, stream=None):
     """fp16(x @ U): x [H, N, D] fp16/bf16, U [H, D, 32] fp16 -> [H, N, 32] fp16."""
     H, N, D = x.shape
-    _check(U, (H, D, RANK), _f16, "U")
+    dev = _dev(x)
+    _check(x, (H, N, D), _HALF, "x", dev)
+    _check(U, (H, D, RANK), _f16, "U", dev)
     if out is None:
-        out = torch.empty(H, N, RANK, dtype=_f16, device=_dev(x))
+        out = torch.empty(H, N, RANK, dtype=_f16, device=dev)
+    _check(out, (H, N, RANK), _f16, "out", dev)
     call("t2t_project", x, dtype_code(x.dtype), U, out, H, N, D, RANK, stream_handle(stream))
     return out
 
@@ -56,11 +94,11 @@ def kmm_run(QU, KU, V, cq0, ck0, *, pin_tail=0, out=None, ws=None, stream=None):
     H, N, r = QU.shape
     CQ, CK = cq0.shape[1], ck0.shape[1]
     dev = _dev(QU)
-    _check(KU, (H, N, r), _f16, "KU")
-    _check(cq0, (H, CQ, r), _f16, "cq0")
-    _check(ck0, (H, CK, r), _f16, "ck0")
-    if V.shape != (H, N, HEAD_DIM):
-        raise ValueError("t2t: V must be [H, N, 128]")
+    _check(QU, (H, N, r), _f16, "QU", dev)
+    _check(KU, (H, N, r), _f16, "KU", dev)
+    _check(cq0, (H, CQ, r), _f16, "cq0", dev)
+    _check(ck0, (H, CK, r), _f16, "ck0", dev)
+    _check(V, (H, N, HEAD_DIM), _HALF, "V", dev)
     o = dict(out or {})
     o.setdefault("qlab", torch.empty(H, N, dtype=_i32, device=dev))
     o.setdefault("cq2", torch.empty(H, CQ, r, dtype=_f16, device=dev))
@@ -73,9 +111,15 @@ def kmm_run(QU, KU, V, cq0, ck0, *, pin_tail=0, out=None, ws=None, stream=None):
     o.setdefault("V_sorted", torch.empty_like(V))
     o.setdefault("sumv", torch.empty(H, CK, HEAD_DIM, dtype=_f16, device=dev))
     o.setdefault("lam", torch.empty(H, dtype=_f32, device=dev))
+    for name, shape, dt in (("qlab", (H, N), _i32), ("cq2", (H, CQ, r), _f16),
+                            ("klab", (H, N), _i32), ("ck2", (H, CK, r), _f32),
+                            ("qcounts", (H, CQ), _i32), ("qperm", (H, N), _i32),
+                            ("kcounts", (H, CK), _i32), ("kperm", (H, N), _i32),
+                            ("V_sorted", (H, N, HEAD_DIM), V.dtype),
+                            ("sumv", (H, CK, HEAD_DIM), _f16), ("lam", (H,), _f32)):
+        _check(o[name], shape, dt, name, dev)
     need = kmm_ws_bytes(H, N, CQ, CK)
-    if ws is None or ws.numel() < need:
-        ws = _ws(need, dev)
+    ws = _ws_for(ws, need, dev)
     call("t2t_kmm_run", QU, KU, V, dtype_code(V.dtype), cq0, ck0, o["qlab"], o["cq2"], o["klab"],
          o["ck2"], o["qcounts"], o["qperm"], o["kcounts"], o["kperm"], o["V_sorted"], o["sumv"],
          o["lam"], H, N, CQ, CK, int(pin_tail), ws, ws.numel(), stream_handle(stream))
@@ -94,9 +138,14 @@ def vstats_gather(V, kperm, kcounts, V_sorted=None, sumv=None, lam=None, ws=None
     V_sorted = torch.empty_like(V) if V_sorted is None else V_sorted
     sumv = torch.empty(H, CK, D, dtype=_f16, device=dev) if sumv is None else sumv
     lam = torch.empty(H, dtype=_f32, device=dev) if lam is None else lam
+    _check(V, (H, N, HEAD_DIM), _HALF, "V", dev)
+    _check(kperm, (H, N), _i32, "kperm", dev)
+    _check(kcounts, (H, CK), _i32, "kcounts", dev)
+    _check(V_sorted, (H, N, HEAD_DIM), V.dtype, "V_sorted", dev)
+    _check(sumv, (H, CK, HEAD_DIM), _f16, "sumv", dev)
+    _check(lam, (H,), _f32, "lam", dev)
     need = vstats_ws_bytes(H, N, CK)
-    if ws is None or ws.numel() < need:
-        ws = _ws(need, dev)
+    ws = _ws_for(ws, need, dev)
     call("t2t_kmm_run_vstats_gather", V, dtype_code(V.dtype), kperm, kcounts, V_sorted, sumv, lam,
          H, N, CK, ws, ws.numel(), stream_handle(stream))
     return V_sorted, sumv, lam
@@ -108,9 +157,12 @@ def vstats(V_sorted, kcounts, sumv=None, lam=None, ws=None, stream=None):
     dev = _dev(V_sorted)
     sumv = torch.empty(H, CK, D, dtype=_f16, device=dev) if sumv is None else sumv
     lam = torch.empty(H, dtype=_f32, device=dev) if lam is None else lam
+    _check(V_sorted, (H, N, HEAD_DIM), _HALF, "V_sorted", dev)
+    _check(kcounts, (H, CK), _i32, "kcounts", dev)
+    _check(sumv, (H, CK, HEAD_DIM), _f16, "sumv", dev)
+    _check(lam, (H,), _f32, "lam", dev)
     need = vstats_ws_bytes(H, N, CK)
-    if ws is None or ws.numel() < need:
-        ws = _ws(need, dev)
+    ws = _ws_for(ws, need, dev)
     call("t2t_kmm_run_vstats", V_sorted, dtype_code(V_sorted.dtype), kcounts, sumv, lam, H, N, CK,
          ws, ws.numel(), stream_handle(stream))
     return sumv, lam
@@ -122,6 +174,9 @@ def centroid_finalize(ck2, scale=1.0 / math.sqrt(HEAD_DIM), ck16=None, cks=None,
     dev = _dev(ck2)
     ck16 = torch.empty(H, CK, r, dtype=_f16, device=dev) if ck16 is None else ck16
     cks = torch.empty(H, CK, r, dtype=_f16, device=dev) if cks is None else cks
+    _check(ck2, (H, CK, r), _f32, "ck2", dev)
+    _check(ck16, (H, CK, r), _f16, "ck16", dev)
+    _check(cks, (H, CK, r), _f16, "cks", dev)
     call("t2t_centroid_finalize", ck2, ck16, cks, float(scale), H, CK, r, stream_handle(stream))
     return ck16, cks
 
@@ -130,13 +185,29 @@ def score(QU, cks, out=None, stream=None):
     """gl = fp16(QU @ cks^T): [H, N, 2048] fp16."""
     H, N, r = QU.shape
     CK = cks.shape[1]
-    out = torch.empty(H, N, CK, dtype=_f16, device=_dev(QU)) if out is None else out
+    dev = _dev(QU)
+    out = torch.empty(H, N, CK, dtype=_f16, device=dev) if out is None else out
+    _check(QU, (H, N, r), _f16, "QU", dev)
+    _check(cks, (H, CK, r), _f16, "cks", dev)
+    _check(out, (H, N, CK), _f16, "out", dev)
     call("t2t_score", QU, cks, out, H, N, CK, r, stream_handle(stream))
     return out
 
 
 def select_ws_bytes(H, N, CQ):
     return size_query("t2t_select_ws_bytes", H, N, CQ)
+
+
+def _check_select(dev, H, N, CQ, *, gl=None, kcounts=None, qperm=None, qcounts=None, unip=None,
+                  rowcnt=None):
+    if gl is not None:
+        _check(gl, (H, N, C_KEYS), _f16, "gl", dev)
+    _check(kcounts, (H, C_KEYS), _i32, "kcounts", dev)
+    _check(qperm, (H, N), _i32, "qperm", dev)
+    _check(qcounts, (H, CQ), _i32, "qcounts", dev)
+    if unip is not None:
+        _check(unip, (H, CQ, C_KEYS // 32), _i32, "unip", dev)
+    _check(rowcnt, (H, N), _i32, "rowcnt", dev)
 
 
 def select_union(gl, kcounts, qperm, qcounts, ns_t, unip=None, rowcnt=None, ws=None,
@@ -149,9 +220,11 @@ def select_union(gl, kcounts, qperm, qcounts, ns_t, unip=None, rowcnt=None, ws=N
         raise ValueError("t2t: selection requires 2048 key clusters")
     unip = torch.empty(H, CQ, CK // 32, dtype=_i32, device=dev) if unip is None else unip
     rowcnt = torch.empty(H, N, dtype=_i32, device=dev) if rowcnt is None else rowcnt
+    _check_select(dev, H, N, CQ, gl=gl, kcounts=kcounts, qperm=qperm, qcounts=qcounts,
+                  unip=unip, rowcnt=rowcnt)
+    _check_ns(ns_t, dev)
     need = select_ws_bytes(H, N, CQ)
-    if ws is None or ws.numel() < need:
-        ws = _ws(need, dev)
+    ws = _ws_for(ws, need, dev)
     if split_cap:
         call("t2t_select_run_split_packed", gl, kcounts, qperm, qcounts, int(split_cap), ns_t, unip,
              rowcnt, H, N, CQ, ws, ws.numel(), stream_handle(stream))
@@ -172,9 +245,13 @@ def score_select(QU, cks, kcounts, qperm, qcounts, ns_t, unip=None, rowcnt=None,
         raise ValueError("t2t: score_select requires cks [H, 2048, 32]")
     unip = torch.empty(H, CQ, C_KEYS // 32, dtype=_i32, device=dev) if unip is None else unip
     rowcnt = torch.empty(H, N, dtype=_i32, device=dev) if rowcnt is None else rowcnt
+    _check(QU, (H, N, RANK), _f16, "QU", dev)
+    _check(cks, (H, C_KEYS, RANK), _f16, "cks", dev)
+    _check_select(dev, H, N, CQ, kcounts=kcounts, qperm=qperm, qcounts=qcounts, unip=unip,
+                  rowcnt=rowcnt)
+    _check_ns(ns_t, dev)
     need = select_ws_bytes(H, N, CQ)
-    if ws is None or ws.numel() < need:
-        ws = _ws(need, dev)
+    ws = _ws_for(ws, need, dev)
     call("t2t_score_select_packed", QU, cks, kcounts, qperm, qcounts, ns_t, unip, rowcnt, H, N, CQ,
          ws, ws.numel(), stream_handle(stream))
     return unip, rowcnt
@@ -188,11 +265,12 @@ def select_union_bytes(gl, kcounts, qperm, qcounts, ns_t, uni=None, rowcnt=None,
     dev = _dev(gl)
     uni = torch.empty(H, CQ, CK, dtype=torch.uint8, device=dev) if uni is None else uni
     rowcnt = torch.empty(H, N, dtype=_i32, device=dev) if rowcnt is None else rowcnt
-    _check(uni, (H, CQ, CK), torch.uint8, "uni")
-    _check(rowcnt, (H, N), _i32, "rowcnt")
+    _check(uni, (H, CQ, CK), torch.uint8, "uni", dev)
+    _check_select(dev, H, N, CQ, gl=gl, kcounts=kcounts, qperm=qperm, qcounts=qcounts,
+                  rowcnt=rowcnt)
+    _check_ns(ns_t, dev)
     need = select_ws_bytes(H, N, CQ)
-    if ws is None or ws.numel() < need:
-        ws = _ws(need, dev)
+    ws = _ws_for(ws, need, dev)
     call("t2t_select_run", gl, kcounts, qperm, qcounts, ns_t, uni, rowcnt, H, N, CQ, ws, ws.numel(),
          stream_handle(stream))
     return uni, rowcnt
@@ -200,6 +278,7 @@ def select_union_bytes(gl, kcounts, qperm, qcounts, ns_t, uni=None, rowcnt=None,
 
 def union_or_last(unip, stream=None):
     H, CQ, W = unip.shape
+    _check(unip, (H, CQ, C_KEYS // 32), _i32, "unip")
     call("t2t_union_or_last", unip, H, CQ, W * 32, stream_handle(stream))
     return unip
 
@@ -207,7 +286,11 @@ def union_or_last(unip, stream=None):
 def fast_gather(x, perm, out=None, stream=None):
     """o[h, i] = x[h, perm[h, i]] for [H, N, D] 16-bit tensors."""
     H, N, D = x.shape
+    dev = _dev(x)
     out = torch.empty_like(x) if out is None else out
+    _check(x, (H, N, D), _HALF, "x", dev)
+    _check(perm, (H, N), _i32, "perm", dev)
+    _check(out, (H, N, D), x.dtype, "out", dev)
     call("t2t_fast_gather", x, dtype_code(x.dtype), perm, out, H, N, D, stream_handle(stream))
     return out
 
@@ -218,8 +301,13 @@ def plan_ints(H, N, CQ):
 
 def tile_plan(qcounts, kcounts, unip, N, plan=None, stream=None):
     H, CQ = qcounts.shape
+    dev = _dev(qcounts)
     if plan is None:
-        plan = torch.empty(plan_ints(H, N, CQ), dtype=_i32, device=_dev(qcounts))
+        plan = torch.empty(plan_ints(H, N, CQ), dtype=_i32, device=dev)
+    _check(qcounts, (H, CQ), _i32, "qcounts", dev)
+    _check(kcounts, (H, C_KEYS), _i32, "kcounts", dev)
+    _check(unip, (H, CQ, C_KEYS // 32), _i32, "unip", dev)
+    _check_plan(plan, H, N, CQ, dev)
     call("t2t_tile_plan", qcounts, kcounts, unip, plan, H, N, CQ, stream_handle(stream))
     return plan
 
@@ -235,6 +323,30 @@ def plan_views(plan, H, N, CQ):
     return dict(k_off=k_off, kvlen=kvlen, ntask=ntask, tasks=tasks)
 
 
+def _check_attn(dev, H, N, CQ, *, q=None, kp=None, vp=None, kcounts=None, unip=None, qperm=None,
+                plan=None, out=None, lse=None, QU=None, cks=None, sumv=None, lam=None, qlab=None,
+                tailw_t=None, qcounts=None, tiles=None, dt=None):
+    qs = (H, N, HEAD_DIM)
+    for name, t, shape, dtype in (
+            ("q", q, qs, _HALF), ("kp", kp, qs, dt), ("vp", vp, qs, dt), ("out", out, qs, dt),
+            ("kcounts", kcounts, (H, C_KEYS), _i32), ("qcounts", qcounts, (H, CQ), _i32),
+            ("unip", unip, (H, CQ, C_KEYS // 32), _i32), ("qperm", qperm, (H, N), _i32),
+            ("qlab", qlab, (H, N), _i32), ("lse", lse, (H, N), _f32),
+            ("QU", QU, (H, N, RANK), _f16), ("cks", cks, (H, C_KEYS, RANK), _f16),
+            ("sumv", sumv, (H, C_KEYS, HEAD_DIM), _f16), ("lam", lam, (H,), _f32),
+            ("tailw_t", tailw_t, (), _f32)):
+        if t is not None:
+            _check(t, shape, dtype, name, dev)
+    if plan is not None:
+        _check_plan(plan, H, N, CQ, dev)
+    if tiles is not None:
+        need = size_query("t2t_centroid_tiles_bytes", H)
+        if (not isinstance(tiles, torch.Tensor) or tiles.dtype != torch.uint8
+                or not tiles.is_contiguous() or tiles.device != dev or tiles.numel() < need):
+            raise ValueError(f"t2t: tiles must be a contiguous uint8 tensor of >= {need} bytes "
+                             f"on {dev}")
+
+
 def tile_attn_exact(q, kp, vp, kcounts, unip, qperm, plan, attn_out=None, lse=None, stream=None):
     """Exact attention over the unions, sorted query order."""
     H, N, D = q.shape
@@ -242,6 +354,8 @@ def tile_attn_exact(q, kp, vp, kcounts, unip, qperm, plan, attn_out=None, lse=No
     dev = _dev(q)
     attn_out = torch.empty_like(q) if attn_out is None else attn_out
     lse = torch.empty(H, N, dtype=_f32, device=dev) if lse is None else lse
+    _check_attn(dev, H, N, CQ, q=q, kp=kp, vp=vp, kcounts=kcounts, unip=unip, qperm=qperm,
+                plan=plan, out=attn_out, lse=lse, dt=q.dtype)
     call("t2t_tile_attn_exact", q, kp, vp, dtype_code(q.dtype), kcounts, unip, qperm, plan,
          attn_out, lse, H, N, CQ, stream_handle(stream))
     return attn_out, lse
@@ -251,10 +365,13 @@ def tail_merge(attn_out, lse, QU, cks, sumv, kcounts, unip, qlab, qperm, lam, ta
                ws=None, stream=None):
     H, N, D = attn_out.shape
     CQ = unip.shape[1]
+    dev = _dev(attn_out)
     out = torch.empty_like(attn_out) if out is None else out
+    _check_attn(dev, H, N, CQ, q=attn_out, out=out, lse=lse, QU=QU, cks=cks, sumv=sumv,
+                kcounts=kcounts, unip=unip, qlab=qlab, qperm=qperm, lam=lam, tailw_t=tailw_t,
+                dt=attn_out.dtype)
     need = size_query("t2t_tail_merge_ws_bytes", H)
-    if ws is None or ws.numel() < need:
-        ws = _ws(need, _dev(attn_out))
+    ws = _ws_for(ws, need, dev)
     call("t2t_tail_merge", attn_out, lse, QU, cks, sumv, kcounts, unip, qlab, qperm, lam, tailw_t,
          out, dtype_code(attn_out.dtype), H, N, CQ, ws, ws.numel(), stream_handle(stream))
     return out
@@ -263,8 +380,10 @@ def tail_merge(attn_out, lse, QU, cks, sumv, kcounts, unip, qlab, qperm, lam, ta
 def centroid_tiles(cks, sumv, tiles=None, stream=None):
     """Tile image of cks / sumv staged by the residual kernel (uint8 bytes)."""
     H = cks.shape[0]
+    dev = _dev(cks)
     need = size_query("t2t_centroid_tiles_bytes", H)
-    tiles = _ws(need, _dev(cks)) if tiles is None else tiles
+    tiles = _ws(need, dev) if tiles is None else tiles
+    _check_attn(dev, H, 0, 0, cks=cks, sumv=sumv, tiles=tiles)
     call("t2t_centroid_tiles", cks, sumv, tiles, H, stream_handle(stream))
     return tiles
 
@@ -273,6 +392,8 @@ def tile_attn_exact_orig(q, kp, vp, kcounts, unip, qperm, plan, out, lse, stream
     """Exact attention written at the original rows of out; lse in sorted order."""
     H, N, D = q.shape
     CQ = unip.shape[1]
+    _check_attn(_dev(q), H, N, CQ, q=q, kp=kp, vp=vp, kcounts=kcounts, unip=unip, qperm=qperm,
+                plan=plan, out=out, lse=lse, dt=q.dtype)
     call("t2t_tile_attn_exact_orig", q, kp, vp, dtype_code(q.dtype), kcounts, unip, qperm, plan,
          out, lse, H, N, CQ, stream_handle(stream))
     return out
@@ -283,6 +404,8 @@ def resid_merge_inplace(out, lse, QU, tiles, kcounts, unip, qlab, qperm, lam, ta
     """Residual + merge into the exact part held at the original rows of out."""
     H, N, D = out.shape
     CQ = unip.shape[1]
+    _check_attn(_dev(out), H, N, CQ, q=out, lse=lse, QU=QU, tiles=tiles, kcounts=kcounts,
+                unip=unip, qlab=qlab, qperm=qperm, lam=lam, tailw_t=tailw_t)
     call("t2t_resid_merge_inplace", out, lse, QU, tiles, kcounts, unip, qlab, qperm, lam, tailw_t,
          dtype_code(out.dtype), H, N, CQ, stream_handle(stream))
     return out
@@ -296,9 +419,12 @@ def tile_attn_run_planned(q, kp, vp, qcounts, kcounts, unip, QU, cks, sumv, lam,
                           tailw_t, out, plan, rebuild, ws=None, stream=None):
     H, N, D = q.shape
     CQ = qcounts.shape[1]
+    dev = _dev(q)
+    _check_attn(dev, H, N, CQ, q=q, kp=kp, vp=vp, qcounts=qcounts, kcounts=kcounts, unip=unip,
+                QU=QU, cks=cks, sumv=sumv, lam=lam, qlab=qlab, qperm=qperm, tailw_t=tailw_t,
+                out=out, plan=plan, dt=q.dtype)
     need = attn_ws_bytes(H, N, q.dtype)
-    if ws is None or ws.numel() < need:
-        ws = _ws(need, _dev(q))
+    ws = _ws_for(ws, need, dev)
     call("t2t_tile_attn_run_planned", q, kp, vp, dtype_code(q.dtype), qcounts, kcounts, unip, QU,
          cks, sumv, lam, qlab, qperm, tailw_t, out, plan, int(bool(rebuild)), H, N, CQ, ws,
          ws.numel(), stream_handle(stream))
@@ -308,7 +434,11 @@ def tile_attn_run_planned(q, kp, vp, qcounts, kcounts, unip, QU, cks, sumv, lam,
 def fast_assign_labels(x, c, out=None, stream=None):
     H, N, D = x.shape
     C = c.shape[1]
-    out = torch.empty(H, N, dtype=_i32, device=_dev(x)) if out is None else out
+    dev = _dev(x)
+    out = torch.empty(H, N, dtype=_i32, device=dev) if out is None else out
+    _check(x, (H, N, D), _f16, "x", dev)
+    _check(c, (H, C, D), _f16, "c", dev)
+    _check(out, (H, N), _i32, "out", dev)
     call("t2t_fast_assign", x, c, out, H, N, C, D, stream_handle(stream))
     return out
 
@@ -318,6 +448,9 @@ def det_centroid_update(x, labels, old, stream=None):
     H, N, D = x.shape
     C = old.shape[1]
     dev = _dev(x)
+    _check(x, (H, N, D), _f16, "x", dev)
+    _check(labels, (H, N), _i32, "labels", dev)
+    _check(old, (H, C, D), _f16, "old", dev)
     new = torch.empty(H, C, D, dtype=_f16, device=dev)
     counts = torch.empty(H, C, dtype=_i32, device=dev)
     ws = _ws(size_query("t2t_det_update_ws_bytes", H, N, C), dev)
@@ -329,6 +462,7 @@ def det_centroid_update(x, labels, old, stream=None):
 def gram(x, stream=None):
     """x^T x / N per head in fp64: [H, D, D]."""
     H, N, D = x.shape
+    _check(x, (H, N, D), _HALF, "x", _dev(x))
     G = torch.empty(H, D, D, dtype=torch.float64, device=_dev(x))
     call("t2t_gram", x, dtype_code(x.dtype), G, H, N, D, stream_handle(stream))
     return G
