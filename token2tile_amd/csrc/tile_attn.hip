@@ -259,13 +259,6 @@ __device__ inline uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
   asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(a), "v"(b));
   return r;
 }
-// an fp16 pair with each half replaced by -inf where its bit of u is set
-// (bits `bit` and `bit` + 1 for the low and high half)
-__device__ inline uint32_t mask_pair_neg_inf(uint32_t pk, uint32_t u, int bit) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_sbfe((int)u, bit, 1);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_sbfe((int)u, bit + 1, 1);
-  return bfi(bfi(0x0000ffffu, lo, hi), 0xfc00fc00u, pk);
-}
 // (b.lo16 << 16) | a.lo16 and (b.hi16 << 16) | a.hi16
 __device__ inline uint32_t pack_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
 __device__ inline uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
@@ -648,7 +641,10 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
     int N, int CQ) {
   __shared__ __attribute__((aligned(1024))) uint16_t sT0[RT_HALVES];
   __shared__ __attribute__((aligned(1024))) uint16_t sT1[RT_HALVES];
-  __shared__ __attribute__((aligned(16))) float sCnt[TA_CK];
+  // counts as fp16, ordered so that the 16 a lane weights in one 32-centroid
+  // half are contiguous: centroid 64 t + 32 kb + 8 j + 4 hh + e sits at
+  // 64 t + 32 kb + 16 hh + 4 j + e
+  __shared__ __attribute__((aligned(16))) uint16_t sCnt[TA_CK];
   const int h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int jl = lane & 31, hh = lane >> 5;
@@ -674,8 +670,11 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
   using B1 = std::integral_constant<int, 1>;
   issue(0, B0{});
 #pragma unroll
-  for (int i = 0; i < TA_CK / 256; ++i)
-    sCnt[tid + 256 * i] = (float)kcounts[(size_t)h * TA_CK + tid + 256 * i];
+  for (int i = 0; i < TA_CK / 256; ++i) {
+    const int c = tid + 256 * i;
+    const int pos = (c & ~31) + 16 * ((c >> 2) & 1) + 4 * ((c >> 3) & 3) + (c & 3);
+    sCnt[pos] = F16T::from_f((float)kcounts[(size_t)h * TA_CK + c]);
+  }
   uint32_t uw0 = ur[0], uw1 = ur[1];
   const float L2E = 1.4426950408889634f;
   float m2 = -1.0e30f, phi = 0.f;
@@ -709,12 +708,25 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
       S = Mfma<F16T>::run(*(const u32x4*)(sb + rc_off(r, hh)), qu0, S);
       S = Mfma<F16T>::run(*(const u32x4*)(sb + rc_off(r, 2 + hh)), qu1, S);
       const uint32_t u = (kb ? uw1 : uw0) >> (4 * hh);  // element a <-> bit 8 (a / 4) + a % 4
+      // pair p = a / 2 reads bits b and b + 1, b = 8 (p / 2) + 2 (p % 2); pairs g
+      // and g + 4 (b and b + 16) share two shifted copies of u: X has bit b at
+      // 15 and b + 16 at 31, Y bits b + 1 and b + 17 there, and v_perm_b32's
+      // sign-replicating selectors (8: X[15], 9: X[31], 10: Y[15], 11: Y[31])
+      // spread each bit over its fp16 half
+      uint32_t mk[8];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int b = 8 * (g >> 1) + 2 * (g & 1);
+        const uint32_t X = u << (15 - b), Y = u << (14 - b);
+        mk[g] = __builtin_amdgcn_perm(Y, X, 0x0a0a0808u);
+        mk[g + 4] = __builtin_amdgcn_perm(Y, X, 0x0b0b0909u);
+      }
       f16x2 sp[8];
       f16x2 mp = {(_Float16)-__builtin_inff(), (_Float16)-__builtin_inff()};
 #pragma unroll
       for (int a = 0; a < 16; a += 2) {
         const uint32_t pk = Pk<F16T>::pack(S[a], S[a + 1]);
-        sp[a / 2] = __builtin_bit_cast(f16x2, mask_pair_neg_inf(pk, u, 8 * (a / 4) + (a % 4)));
+        sp[a / 2] = __builtin_bit_cast(f16x2, bfi(mk[a / 2], 0xfc00fc00u, pk));
         mp = __builtin_elementwise_maximum(mp, sp[a / 2]);
       }
       float mx = vmax((float)mp[0], (float)mp[1]);
@@ -731,18 +743,28 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
           for (int a = 0; a < 16; ++a) O[nb][a] *= alpha;
       }
       const float nm = -m2 * L2E;
+      // P as fp16 pairs; the count-weighted sum takes the same rounded P
+      // through v_dot2_f32_f16 (the counts are exact in fp16 up to 2048)
       u32x4 pb[2];
+      const u32x4* cw = (const u32x4*)(sCnt + TL_CT * tc + 32 * kb + 16 * hh);
+      const u32x4 cn0 = cw[0], cn1 = cw[1];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const f32x4 cn = *(const f32x4*)(sCnt + TL_CT * tc + 32 * kb + 8 * j + 4 * hh);
         float pe[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
+        for (int e = 0; e < 4; ++e)
           pe[e] = __builtin_amdgcn_exp2f(fmaf((float)sp[2 * j + e / 2][e % 2], L2E, nm));
-          phi = fmaf(pe[e], cn[e], phi);
-        }
-        pb[j / 2][2 * (j % 2)] = Pk<F16T>::pack(pe[0], pe[1]);
-        pb[j / 2][2 * (j % 2) + 1] = Pk<F16T>::pack(pe[2], pe[3]);
+        const uint32_t p01 = Pk<F16T>::pack(pe[0], pe[1]), p23 = Pk<F16T>::pack(pe[2], pe[3]);
+        pb[j / 2][2 * (j % 2)] = p01;
+        pb[j / 2][2 * (j % 2) + 1] = p23;
+        // (copied to scalars first: a bit_cast straight from a vector element
+        // reads element 0)
+        const uint32_t c01 = (j < 2 ? cn0 : cn1)[2 * (j % 2)];
+        const uint32_t c23 = (j < 2 ? cn0 : cn1)[2 * (j % 2) + 1];
+        phi = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p01), __builtin_bit_cast(f16x2, c01),
+                                     phi, false);
+        phi = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p23), __builtin_bit_cast(f16x2, c23),
+                                     phi, false);
       }
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
