@@ -202,6 +202,15 @@ int t2t_tile_attn_exact_orig(const void* q, const void* kp, const void* vp, int 
                              const int32_t* kcounts, const int32_t* unip, const int32_t* qperm,
                              const int32_t* plan, void* out, float* lse,
                              int H, int N, int CQ, void* stream);
+/* t2t_tile_attn_exact_orig with the K gather fused into the kernel's loads:
+ * k is [H, N, 128] in the ORIGINAL order and key position p of the cluster
+ * order reads row kperm[h, p], so kp = k[kperm] is never stored.  Replaces
+ * the fast_gather of deploy_step.py:326,456 together with the attention
+ * launch that reads its output (tile_attn/src/kernel.cu:820-1096). */
+int t2t_tile_attn_exact_orig_gather(const void* q, const void* k, const int32_t* kperm,
+                                    const void* vp, int dtype, const int32_t* kcounts,
+                                    const int32_t* unip, const int32_t* qperm, const int32_t* plan,
+                                    void* out, float* lse, int H, int N, int CQ, void* stream);
 /* Residual + merge into the exact part held at the original rows of out
  * (S6); tiles from t2t_centroid_tiles.  With the two entries above, the
  * steps of t2t_tile_attn_run_planned one launch at a time. */

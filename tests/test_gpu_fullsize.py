@@ -81,7 +81,8 @@ def test_full_size_call(dev, name, dtype):
         ident = np.arange(64, dtype=np.int32)[None]
         up = unip[h, tq][None]
         qh = q[h, torch.from_numpy(qs).to(dev)].float().cpu().numpy()[None]
-        kp = io["kp"][h].float().cpu().numpy()[None]
+        # K in cluster order, read by the kernel through kperm
+        kp = k[h][last["kperm"][h].long()].float().cpu().numpy()[None]
         vp = io["vp"][h].float().cpu().numpy()[None]
         ao, lse = O.tile_attention(qh, kp, vp, one, kcounts[h][None], up, ident)
         QU = op.QU[h, torch.from_numpy(qs).to(dev)].cpu().numpy()[None]

@@ -359,6 +359,26 @@ def test_full_union_equals_sdpa(dev):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_exact_orig_gather_equals_gathered(dev, dtype):
+    """Exact attention with K read through kperm == the same kernel over
+    kp = k[kperm], bit for bit (empty clusters and a partial last tile
+    included in the case)."""
+    from token2tile_amd import ops
+    rng = np.random.default_rng(21)
+    q, k, v, kperm, kcounts, qlab, qperm, qcounts, unip, kp, vp = attn_case(rng)
+    H, N, _ = q.shape
+    tq, tk, tkp, tvp = (g(a, dev).to(dtype) for a in (q, k, kp, vp))
+    plan = ops.tile_plan(g(qcounts, dev), g(kcounts, dev), g(unip, dev), N)
+    args = (g(kcounts, dev), g(unip, dev), g(qperm, dev), plan)
+    out_a, lse_a = torch.zeros_like(tq), torch.zeros(H, N, dtype=torch.float32, device=dev)
+    out_b, lse_b = torch.zeros_like(tq), torch.zeros(H, N, dtype=torch.float32, device=dev)
+    ops.tile_attn_exact_orig(tq, tkp, tvp, *args, out_a, lse_a)
+    ops.tile_attn_exact_orig_gather(tq, tk, g(kperm, dev), tvp, *args, out_b, lse_b)
+    assert torch.equal(out_a, out_b) and torch.equal(lse_a, lse_b)
+    assert int(kcounts.min()) == 0  # the case holds empty key clusters
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_tail_merge(dev, dtype):
     from token2tile_amd import ops
     rng = np.random.default_rng(11)

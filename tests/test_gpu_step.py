@@ -107,6 +107,30 @@ def test_pin_tail_and_determinism(dev):
     assert np.abs(o - eo).max() <= 2e-2 and cos(o, eo) >= 0.999
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_k_gather_is_bit_identical(dev, dtype):
+    """The attention kernel reading K through kperm gives the same bits as
+    the separate gather kp = k[kperm] followed by the attention over kp, on a
+    full call and on a reuse call (the gather is a pure copy of rows)."""
+    deploy, q, k, v = make(dev, mask_refresh=4)
+    tq, tk, tv = (torch.from_numpy(a).to(dev).to(dtype) for a in (q, k, v))
+    state = deploy.init_state(tq, tk, seed=4)
+    outs = {}
+    for fused in (True, False):
+        deploy.fuse_k_gather = fused
+        st = {k_: v_.clone() for k_, v_ in state.items()}
+        deploy.reset_cfg_reuse()
+        deploy.set_cfg_call(0, key=1, step=0)
+        full = deploy.step(tq, tk, tv, st).clone()
+        assert deploy.last_call_full
+        deploy.set_cfg_call(1, key=1, step=0)
+        reuse = deploy.step(tq, tk, tv, st).clone()
+        assert not deploy.last_call_full
+        outs[fused] = (full, reuse)
+    assert torch.equal(outs[True][0], outs[False][0])
+    assert torch.equal(outs[True][1], outs[False][1])
+
+
 def test_bad_inputs_raise(dev):
     from token2tile_amd.deploy_step import MaskedStepDeploy
     with pytest.raises(ValueError):

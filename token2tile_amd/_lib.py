@@ -51,6 +51,8 @@ SIGNATURES = {
     "t2t_centroid_tiles": (c_int, [_P, _P, _P, c_int, _P]),
     "t2t_tile_attn_exact_orig": (c_int, [_P, _P, _P, c_int, _P, _P, _P, _P, _P, _P, c_int, c_int,
                                          c_int, _P]),
+    "t2t_tile_attn_exact_orig_gather": (c_int, [_P, _P, _P, _P, c_int, _P, _P, _P, _P, _P, _P,
+                                                c_int, c_int, c_int, _P]),
     "t2t_resid_merge_inplace": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int,
                                         c_int, c_int, _P]),
     "t2t_tail_merge_ws_bytes": (c_size_t, [c_int]),

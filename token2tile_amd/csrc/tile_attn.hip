@@ -268,6 +268,8 @@ __device__ inline uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_am
 // One work-group (4 waves, 32 queries each) per task of <= 128 queries, two
 // work-groups per CU.  MODE 0: attn_out and lse (log2 units) in sorted order.
 // MODE 1: the exact output at the original rows of out, lse in sorted order
+// MODE 2: as MODE 1, with the K gather fused: kp is k in its original order and
+// key position p of cluster order reads row kperm[p] (no separate kp = k[kperm])
 // (the residual kernel merges into out in place).
 template <typename T, int MODE>
 __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
@@ -276,7 +278,8 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     const int32_t* __restrict__ qperm, const int32_t* __restrict__ kcounts,
     const int32_t* __restrict__ k_off, const int32_t* __restrict__ ntask,
     const int32_t* __restrict__ tasks, uint16_t* __restrict__ attn_out, float* __restrict__ lse,
-    uint16_t* __restrict__ out, int H, int N, int CQ, int maxT) {
+    uint16_t* __restrict__ out, const int32_t* __restrict__ kperm, int H, int N, int CQ, int maxT) {
+  constexpr bool KG = MODE == 2;
   // two separate arrays (not one [2][...] array): the K DMA into one buffer
   // must not be taken as a possible writer of the other one, or every read of
   // the tile in use would wait for the loads of the tile in flight
@@ -290,6 +293,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
   __shared__ uint16_t runCumLo[TA_CK + 1], runRowLo[TA_CK];
   __shared__ uint8_t runCumHi[TA_CK + 1], runRowHi[TA_CK];
   __shared__ int sIdx[2][TA_KT];
+  __shared__ int sIdxK[KG ? 2 : 1][KG ? TA_KT : 1];  // MODE 2: K source rows (original order)
   __shared__ int bMark[TA_KT];
   __shared__ int wsc[TA_WAVES], wsr[TA_WAVES];
   const int total = H * maxT;
@@ -416,6 +420,10 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     // marks the tile slot where that run starts; a prefix max over the marks
     // gives each position its run.
     int r0 = 0;
+    // MODE 2: the K rows of the tile last built, loaded from kperm by the
+    // index wave and stored to sIdxK after the next wait on the memory counter
+    int kpend = 0;
+    const int32_t* kph = KG ? kperm + (size_t)h * N : nullptr;
     auto build_idx = [&](int tile) {
       if (wave == TA_WAVES - 1) {
         const int base = tile * TA_KT;
@@ -433,7 +441,9 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
         const int k = wave_incl_max(bMark[lane] - 1);
         const int pos = base + lane;
         const int ck = __shfl(cs, k, 64), rk = __shfl(rw, k, 64);
-        sIdx[tile & 1][lane] = pos < kvlen ? rk + pos - ck : 0;
+        const int vrow = pos < kvlen ? rk + pos - ck : 0;
+        sIdx[tile & 1][lane] = vrow;
+        if constexpr (KG) kpend = pos < kvlen ? kph[vrow] : 0;
         // run holding the next tile's first position: the last run starting at
         // or before it.  The lanes see runs r0 .. r0 + 63 only; when all of
         // them qualify (64 runs of one key each), run r0 + 64 may start exactly
@@ -443,6 +453,10 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
         if (seen == 64 && r0 + 64 < nrun && run_cum(r0 + 64) <= base + TA_KT) nxt = r0 + 64;
         r0 = nxt;
       }
+    };
+    auto flush_k = [&](int tile) {
+      if constexpr (KG)
+        if (wave == TA_WAVES - 1) sIdxK[tile & 1][lane] = kpend;
     };
     // K and V tiles via LDS DMA (each wave instruction fills 4 whole rows, the
     // lane fetching the 16-byte chunk that belongs at its swizzled position)
@@ -455,7 +469,8 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
         const int blk = 4 * i + wave;
         const int row = 4 * blk + (lane >> 4);
         const uint32_t base = (uint32_t)sIdx[buf][row] * 256u;
-        const uint32_t offk = base + 16u * ((lane & 15) ^ (row & 15));
+        const uint32_t kbase = KG ? (uint32_t)sIdxK[buf][row] * 256u : base;
+        const uint32_t offk = kbase + 16u * ((lane & 15) ^ (row & 15));
         const uint32_t offv = base + 16u * ((lane & 15) ^ sv_swz(row));
         __builtin_amdgcn_global_load_lds((const glb_void_t*)(kh + offk),
                                          (lds_void_t*)(sKb + blk * 4 * 128), 16, 0, 0);
@@ -518,7 +533,11 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     using B1 = std::integral_constant<int, 1>;
     __syncthreads();  // runs visible
     build_idx(0);
-    if (ntile > 1) build_idx(1);
+    flush_k(0);
+    if (ntile > 1) {
+      build_idx(1);
+      flush_k(1);
+    }
     __syncthreads();
     issue(0, B0{});
     __builtin_amdgcn_s_waitcnt(0);
@@ -530,7 +549,8 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     auto body = [&](int tile, auto BUF) {
       constexpr int buf = decltype(BUF)::value;
       if (wave_active) tile_step(BUF, TA_KT, std::false_type{});
-      __builtin_amdgcn_s_waitcnt(0);  // K and V DMA of tile + 1 landed
+      __builtin_amdgcn_s_waitcnt(0);  // K and V DMA of tile + 1 landed (and kperm of tile + 2)
+      if (tile + 2 < ntile) flush_k(tile + 2);
       __syncthreads();
       if (tile + 2 < ntile) issue(tile + 2, BUF);
       if (tile + 3 < ntile) build_idx(tile + 3);
@@ -577,13 +597,13 @@ template <typename T, int MODE>
 static void launch_attn(const void* q, const void* kp, const void* vp, const int32_t* unip,
                         const int32_t* qperm, const int32_t* kcounts, const PlanView& p,
                         void* attn_out, float* lse, void* out, int H, int N, int CQ,
-                        hipStream_t st) {
+                        hipStream_t st, const int32_t* kperm = nullptr) {
   const int total = H * p.maxT;
   const int grid = ((total + 63) / 64) * 64;
   hipLaunchKernelGGL((attn_kernel<T, MODE>), dim3(grid), dim3(TA_WAVES * 64), 0, st,
                      (const uint16_t*)q, (const uint16_t*)kp, (const uint16_t*)vp,
                      (const uint32_t*)unip, qperm, kcounts, p.k_off, p.ntask, p.tasks,
-                     (uint16_t*)attn_out, lse, (uint16_t*)out, H, N, CQ, p.maxT);
+                     (uint16_t*)attn_out, lse, (uint16_t*)out, kperm, H, N, CQ, p.maxT);
 }
 
 // ---------------------------------------------------------------------------
@@ -902,6 +922,26 @@ extern "C" int t2t_centroid_tiles(const void* cks, const void* sumv, void* tiles
   T2T_REQUIRE(H > 0, "centroid_tiles: H=%d", H);
   launch_centroid_tiles(cks, sumv, tiles, H, (hipStream_t)stream);
   T2T_LAUNCH_CHECK("centroid_tiles");
+  return T2T_OK;
+}
+
+extern "C" int t2t_tile_attn_exact_orig_gather(const void* q, const void* k, const int32_t* kperm,
+                                               const void* vp, int dtype, const int32_t* kcounts,
+                                               const int32_t* unip, const int32_t* qperm,
+                                               const int32_t* plan, void* out, float* lse, int H,
+                                               int N, int CQ, void* stream) {
+  T2T_REQUIRE(q && k && kperm && vp && kcounts && unip && qperm && plan && out && lse,
+              "tile_attn_exact_orig_gather: null pointer");
+  T2T_REQUIRE(check_dtype(dtype), "tile_attn_exact_orig_gather: dtype %d", dtype);
+  T2T_REQUIRE(H > 0 && N > 0 && N < (1 << 24) && CQ > 0,
+              "tile_attn_exact_orig_gather: H=%d N=%d CQ=%d", H, N, CQ);
+  PlanView p = plan_view((int32_t*)plan, H, N, CQ);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == T2T_F16)
+    launch_attn<F16T, 2>(q, k, vp, unip, qperm, kcounts, p, nullptr, lse, out, H, N, CQ, st, kperm);
+  else
+    launch_attn<BF16T, 2>(q, k, vp, unip, qperm, kcounts, p, nullptr, lse, out, H, N, CQ, st, kperm);
+  T2T_LAUNCH_CHECK("tile_attn_exact_orig_gather");
   return T2T_OK;
 }
 

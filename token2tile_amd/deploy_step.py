@@ -164,6 +164,9 @@ class MaskedStepDeploy:
         self._io = {}                 # dtype -> (kp, vp, out, attn workspace)
         self._tile_attn_plan_ints = ops.plan_ints(H, N, CQ)
         self.tailw_t = torch.tensor(float(tailw), device=dev, dtype=f32)
+        # the exact-attention kernel reads K through kperm (kp = k[kperm] is
+        # not materialised); False restores the reference's separate gather
+        self.fuse_k_gather = True
         self._kmm_cq2 = torch.empty(H, CQ, r, device=dev, dtype=f16)
         self._kmm_ck2 = torch.empty(H, C, r, device=dev, dtype=f32)
         self._kmm_kcounts = torch.empty(H, C, device=dev, dtype=i32)
@@ -215,16 +218,24 @@ class MaskedStepDeploy:
         io = self._io.get(dtype)
         if io is None:
             H, N, D = self.H, self.N, self.D
-            io = dict(kp=torch.empty(H, N, D, device=self.dev, dtype=dtype),
+            io = dict(kp=None,  # allocated on first use (the fused gather needs none)
                       vp=torch.empty(H, N, D, device=self.dev, dtype=dtype),
                       out=torch.empty(H, N, D, device=self.dev, dtype=dtype),
                       attn_out=None, lse=None)
             self._io[dtype] = io
         return io
 
+    def _kp(self, dtype):
+        io = self._buffers(dtype)
+        if io["kp"] is None:
+            io["kp"] = torch.empty(self.H, self.N, self.D, device=self.dev, dtype=dtype)
+        return io["kp"]
+
     @property
     def kp(self):
-        return self._buffers(torch.float16)["kp"]
+        """The cluster-ordered K buffer; written by ``step`` only when
+        ``fuse_k_gather`` is off (the fused kernel reads k through kperm)."""
+        return self._kp(torch.float16)
 
     @property
     def vp(self):
@@ -314,8 +325,9 @@ class MaskedStepDeploy:
                 # the stored kperm, fresh value statistics from this call's V
                 with self._stage("project"):
                     ops.project(q, snap["Uq"], out=self.QU, stream=s0)
-                with self._stage("gather_k"):
-                    ops.fast_gather(k, snap["kperm"], out=io["kp"], stream=s0)
+                if not self.fuse_k_gather:
+                    with self._stage("gather_k"):
+                        ops.fast_gather(k, snap["kperm"], out=self._kp(k.dtype), stream=s0)
                 kperm = snap["kperm"]
                 with self._stage("vstats"):
                     ops.vstats_gather(v, snap["kperm"], snap["counts"], V_sorted=io["vp"],
@@ -359,8 +371,9 @@ class MaskedStepDeploy:
                                      rowcnt=self.rowcnt, ws=self._ws_sel, stream=s0)
                     if self.pin_tail:
                         ops.union_or_last(unip, stream=s0)
-                with self._stage("gather_k"):
-                    ops.fast_gather(k, km_out["kperm"], out=io["kp"], stream=s0)
+                if not self.fuse_k_gather:
+                    with self._stage("gather_k"):
+                        ops.fast_gather(k, km_out["kperm"], out=self._kp(k.dtype), stream=s0)
                 kperm = km_out["kperm"]
                 plan = (held["tile_attn_plan"] if recycle else
                         torch.empty(self._tile_attn_plan_ints, device=self.dev, dtype=torch.int32))
@@ -389,8 +402,12 @@ class MaskedStepDeploy:
             with self._stage("attention_prep"):
                 ops.centroid_tiles(cks, self._kmm_sumv, tiles=self._ctiles, stream=s0)
             with self._stage("attention_exact"):
-                ops.tile_attn_exact_orig(q, io["kp"], io["vp"], counts, unip, qperm, plan,
-                                         io["out"], self._lse, stream=s0)
+                if self.fuse_k_gather:
+                    ops.tile_attn_exact_orig_gather(q, k, kperm, io["vp"], counts, unip, qperm, plan,
+                                                    io["out"], self._lse, stream=s0)
+                else:
+                    ops.tile_attn_exact_orig(q, io["kp"], io["vp"], counts, unip, qperm, plan,
+                                             io["out"], self._lse, stream=s0)
             with self._stage("attention_residual"):
                 ops.resid_merge_inplace(io["out"], self._lse, self.QU, self._ctiles, counts, unip,
                                         qlab_cur, qperm, self._kmm_lam, self.tailw_t, stream=s0)

@@ -399,6 +399,20 @@ def tile_attn_exact_orig(q, kp, vp, kcounts, unip, qperm, plan, out, lse, stream
     return out
 
 
+def tile_attn_exact_orig_gather(q, k, kperm, vp, kcounts, unip, qperm, plan, out, lse, stream=None):
+    """tile_attn_exact_orig reading K in place: k in the original order, key
+    position p of the cluster order at row kperm[h, p] (no kp = k[kperm])."""
+    H, N, D = q.shape
+    CQ = unip.shape[1]
+    dev = _dev(q)
+    _check_attn(dev, H, N, CQ, q=q, kp=k, vp=vp, kcounts=kcounts, unip=unip, qperm=qperm,
+                plan=plan, out=out, lse=lse, dt=q.dtype)
+    _check(kperm, (H, N), _i32, "kperm", dev)
+    call("t2t_tile_attn_exact_orig_gather", q, k, kperm, vp, dtype_code(q.dtype), kcounts, unip,
+         qperm, plan, out, lse, H, N, CQ, stream_handle(stream))
+    return out
+
+
 def resid_merge_inplace(out, lse, QU, tiles, kcounts, unip, qlab, qperm, lam, tailw_t,
                         stream=None):
     """Residual + merge into the exact part held at the original rows of out."""
