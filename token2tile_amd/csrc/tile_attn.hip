@@ -224,8 +224,6 @@ __device__ inline int xcd_remap(int bid, int total) {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
-typedef short v4i16_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
 // LDS tile layouts (no padding, XOR swizzles keep the MFMA operand reads
 // conflict free):
@@ -367,25 +365,60 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
   // (l % 16) / 4 at dims D + 4 (l % 4) .. + 3, D = 32 nb + 16 ((l / 16) % 2),
   // and so receives dim D + l % 16 of keys 16 mm + 8 r + 4 hh + 0 .. 3: the
   // operand elements t = 4 r + k, which hold keys 8 (t / 4) + 4 hh + t % 4 of
-  // the k-step, the order the P fragments are packed in.
+  // the k-step, the order the P fragments are packed in.  The swizzle of key
+  // 16 mm + 8 r + trkey depends on trkey alone, so one address per dim block
+  // nb serves all eight reads of the block, with mm and r as immediate
+  // offsets of (16 mm + 8 r) * 256 bytes.
   const int trkey = 4 * hh + ((lane & 15) >> 2);
   const int trdim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  // P.V with the transposing reads in inline assembly: the compiler's own
+  // form of this read waits on every in-flight vector-memory load (the next
+  // tile's K/V DMA) before it, cutting that DMA's latency budget to half a
+  // tile.  The reads of dim block nb + 1 are issued before the MFMAs of nb,
+  // and an explicit lgkmcnt wait that names nb's fragments as its operands
+  // orders those MFMAs after their data (no other LDS access is in flight).
   auto pv = [&](f32x16 (&Oa)[4], const uint16_t* sVb, const u32x4 (&pb)[4]) {
+    const uint32_t vbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)sVb;
+    uint32_t ad[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+      ad[nb] = vbase + 2u * (uint32_t)(trkey * 128 + 8 * ((4 * nb + (trdim >> 3)) ^ sv_swz(trkey)) + (trdim & 7));
+    u32x2 fr[2][8];
+    auto rd8 = [&](u32x2 (&f)[8], uint32_t a) {
+      asm volatile(
+          "ds_read_b64_tr_b16 %0, %8\n\t"
+          "ds_read_b64_tr_b16 %1, %8 offset:2048\n\t"
+          "ds_read_b64_tr_b16 %2, %8 offset:4096\n\t"
+          "ds_read_b64_tr_b16 %3, %8 offset:6144\n\t"
+          "ds_read_b64_tr_b16 %4, %8 offset:8192\n\t"
+          "ds_read_b64_tr_b16 %5, %8 offset:10240\n\t"
+          "ds_read_b64_tr_b16 %6, %8 offset:12288\n\t"
+          "ds_read_b64_tr_b16 %7, %8 offset:14336"
+          : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]),
+            "=&v"(f[6]), "=&v"(f[7])
+          : "v"(a));
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    rd8(fr[0], ad[0]);
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
+      u32x2 (&f)[8] = fr[nb & 1];
+      if (nb + 1 < 4) {
+        rd8(fr[(nb + 1) & 1], ad[nb + 1]);
+        asm volatile("s_waitcnt lgkmcnt(8)"
+                     : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]),
+                       "+v"(f[6]), "+v"(f[7]));
+      } else {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]),
+                       "+v"(f[6]), "+v"(f[7]));
+      }
 #pragma unroll
       for (int mm = 0; mm < 4; ++mm) {
-        u32x2 part[2];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          const int key = 16 * mm + 8 * r + trkey, dim = 32 * nb + trdim;
-          const uint16_t* src = sVb + key * 128 + 8 * ((dim >> 3) ^ sv_swz(key)) + (dim & 7);
-          part[r] = __builtin_bit_cast(
-              u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)src));
-        }
-        const u32x4 a = {part[0][0], part[0][1], part[1][0], part[1][1]};
+        const u32x4 a = {f[2 * mm][0], f[2 * mm][1], f[2 * mm + 1][0], f[2 * mm + 1][1]};
         Oa[nb] = Mfma<T>::run(a, pb[mm], Oa[nb]);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
   auto rescale = [&](f32x16 (&Oa)[4], float alpha) {
@@ -482,16 +515,33 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     auto tile_step = [&](auto BUF, int valid, auto MASK) {
       constexpr int buf = decltype(BUF)::value;
       const uint16_t* sKb = buf ? sK1 : sK0;
-      f32x16 S[2];
+      // scores of the two 32-key halves as two interleaved MFMA chains, each
+      // chain's K fragment read four steps ahead.  The scheduling barriers
+      // keep that order: left alone, the compiler read one chain ahead into
+      // spare registers and fed the other through a single buffer, each MFMA
+      // of it waiting on its own LDS read.
+      f32x16 S[2] = {zero16(), zero16()};
+      auto rdk = [&](int kb, int s) {
+        return *(const u32x4*)(sKb + sk_off(32 * kb + jl, 2 * s + hh));
+      };
+      constexpr int KD = 4;  // read-ahead depth in k-steps
+      u32x4 f0[KD], f1[KD];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        S[kb] = zero16();
+      for (int s = 0; s < KD; ++s) {
+        f0[s] = rdk(0, s);
+        f1[s] = rdk(1, s);
+      }
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const u32x4 a = *(const u32x4*)(sKb + sk_off(32 * kb + jl, 2 * s + hh));
-          S[kb] = Mfma<T>::run(a, qb[s], S[kb]);
+      for (int s = 0; s < 8; ++s) {
+        __builtin_amdgcn_sched_barrier(0);
+        S[0] = Mfma<T>::run(f0[s % KD], qb[s], S[0]);
+        S[1] = Mfma<T>::run(f1[s % KD], qb[s], S[1]);
+        if (s + KD < 8) {
+          f0[s % KD] = rdk(0, s + KD);
+          f1[s % KD] = rdk(1, s + KD);
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
       if constexpr (decltype(MASK)::value) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
