@@ -319,12 +319,17 @@ class MaskedStepDeploy:
         recycle = held is not None and snap is None
         self.last_call_full = snap is None
 
+        qu_ready = None
         with torch.cuda.stream(s0):
             if snap is not None:
                 # reuse: project with the snapshot's Uq, group K and V through
-                # the stored kperm, fresh value statistics from this call's V
-                with self._stage("project"):
-                    ops.project(q, snap["Uq"], out=self.QU, stream=s0)
+                # the stored kperm, fresh value statistics from this call's V.
+                # Only the residual reads QU, so the projection runs on the
+                # side stream, under the V statistics and the exact attention.
+                s1.wait_stream(s0)
+                ops.project(q, snap["Uq"], out=self.QU, stream=s1)
+                qu_ready = torch.cuda.Event()
+                qu_ready.record(s1)
                 if not self.fuse_k_gather:
                     with self._stage("gather_k"):
                         ops.fast_gather(k, snap["kperm"], out=self._kp(k.dtype), stream=s0)
@@ -408,6 +413,8 @@ class MaskedStepDeploy:
                 else:
                     ops.tile_attn_exact_orig(q, io["kp"], io["vp"], counts, unip, qperm, plan,
                                              io["out"], self._lse, stream=s0)
+            if qu_ready is not None:
+                s0.wait_event(qu_ready)
             with self._stage("attention_residual"):
                 ops.resid_merge_inplace(io["out"], self._lse, self.QU, self._ctiles, counts, unip,
                                         qlab_cur, qperm, self._kmm_lam, self.tailw_t, stream=s0)
