@@ -42,6 +42,9 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-dense", action="store_true")
     p.add_argument("--sdpa", action="store_true", help="also time torch SDPA (slow at 720p)")
+    p.add_argument("--calibrate", action="store_true",
+                   help="run one row-permuting copy of K (gather_rows_kernel, known bytes) before "
+                        "the warm-up, as the scale reference of FETCH_SIZE/WRITE_SIZE counter runs")
     return p.parse_args()
 
 
@@ -107,6 +110,12 @@ def main():
     torch.cuda.synchronize()
     init_ms = (time.perf_counter() - t0) * 1e3
     print(f"[bench] init_state {init_ms:.1f} ms", file=sys.stderr, flush=True)
+    if args.calibrate:
+        # reads H*N*256 B of k plus the H*N int32 permutation, writes H*N*256 B
+        perm = torch.argsort(torch.rand(H, N, device=dev), dim=1).to(torch.int32)
+        ops.fast_gather(k, perm, out=torch.empty_like(k))
+        torch.cuda.synchronize()
+        del perm
 
     step_no = [0]
 
