@@ -299,28 +299,51 @@ __global__ __launch_bounds__(256) void fixed_mean_kernel(const uint16_t* __restr
   if (c >= C) return;
   const int n = counts[(size_t)h * C + c];
   const int b = cbase[(size_t)h * C + c];
-  const int d = l & 31, par = l >> 5;
+  // lane l sums dims 4 (l % 8) .. + 3 of rows i with i % 8 = l / 8: the
+  // cluster's row indices are read 64 at a time (one coalesced load) and
+  // broadcast, so eight independent row loads are in flight per lane.  The
+  // sums are exact integers, so their order does not change the result.
+  const int dq = l & 7, rg = l >> 3;
   const float scale = MODE == 0 ? 32768.0f : 1048576.0f;
-  long long S = 0;
+  long long S[4] = {0, 0, 0, 0};
   const int32_t* ph = perm + (size_t)h * N + b;
-  const uint16_t* xh = X + (size_t)h * N * KM_R;
-  for (int i = par; i < n; i += 2) {
-    const int row = ph[i];
-    S += (long long)rintf(h2f(xh[(size_t)row * KM_R + d]) * scale);
-  }
-  S += __shfl_xor(S, 32, 64);
-  if (par == 0) {
-    const size_t o = ((size_t)h * C + c) * KM_R + d;
-    uint16_t v;
-    if (n == 0) {
-      v = old[o];
-    } else if (MODE == 0) {
-      v = f2h(opaque((float)S / (32768.0f * (float)n)));
-    } else {
-      const double m = ((double)S / 1048576.0) / (double)n;
-      v = f2h(opaque((float)m));
+  const uint16_t* xh = X + (size_t)h * N * KM_R + 4 * dq;
+  for (int i0 = 0; i0 < n; i0 += 64) {
+    const int myrow = i0 + l < n ? ph[i0 + l] : -1;
+    u32x2 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int row = __shfl(myrow, 8 * j + rg, 64);
+      v[j] = row >= 0 ? *(const u32x2*)(xh + (size_t)row * KM_R) : u32x2{0u, 0u};
     }
-    out[o] = v;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint16_t x = (uint16_t)(v[j][e >> 1] >> (16 * (e & 1)));
+        S[e] += (long long)rintf(h2f(x) * scale);
+      }
+  }
+  // sum over the eight row groups (lane bits 3..5)
+#pragma unroll
+  for (int m = 8; m < 64; m <<= 1)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) S[e] += __shfl_xor(S[e], m, 64);
+  if (rg == 0) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const size_t o = ((size_t)h * C + c) * KM_R + 4 * dq + e;
+      uint16_t v;
+      if (n == 0) {
+        v = old[o];
+      } else if (MODE == 0) {
+        v = f2h(opaque((float)S[e] / (32768.0f * (float)n)));
+      } else {
+        const double m = ((double)S[e] / 1048576.0) / (double)n;
+        v = f2h(opaque((float)m));
+      }
+      out[o] = v;
+    }
   }
 }
 
