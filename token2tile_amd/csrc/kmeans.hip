@@ -370,17 +370,19 @@ __global__ __launch_bounds__(256) void key_gather_kernel(
   const uint16_t* kh = KU ? KU + (size_t)h * N * KM_R : nullptr;
   const uint32_t* vh = (const uint32_t*)(V + (size_t)h * N * 128);
   uint32_t* vsh = V_sorted ? (uint32_t*)(V_sorted + (size_t)h * N * 128) : nullptr;
-  float ax = 0.f, v0 = 0.f, v1 = 0.f;
+  // lanes 0..15 also sum the projected key rows, dims 2 l and 2 l + 1 (one
+  // 4-byte load per row; each dim still sums its rows in order)
+  float ax0 = 0.f, ax1 = 0.f, v0 = 0.f, v1 = 0.f;
+  const uint32_t* kh32 = (const uint32_t*)kh;
   for (int i = 0; i < n; i += KG_UNR) {
     int rw[KG_UNR];
-    uint32_t vv[KG_UNR];
-    float xv[KG_UNR];
+    uint32_t vv[KG_UNR], xv[KG_UNR];
 #pragma unroll
     for (int u = 0; u < KG_UNR; ++u) rw[u] = (i + u < n) ? (ph ? ph[i + u] : b + i + u) : -1;
 #pragma unroll
     for (int u = 0; u < KG_UNR; ++u) {
       vv[u] = rw[u] >= 0 ? __builtin_nontemporal_load(&vh[(size_t)rw[u] * 64 + l]) : 0u;
-      xv[u] = (kh && rw[u] >= 0 && l < 32) ? h2f(kh[(size_t)rw[u] * KM_R + l]) : 0.f;
+      xv[u] = (kh32 && rw[u] >= 0 && l < 16) ? kh32[(size_t)rw[u] * (KM_R / 2) + l] : 0u;
     }
 #pragma unroll
     for (int u = 0; u < KG_UNR; ++u) {
@@ -388,7 +390,8 @@ __global__ __launch_bounds__(256) void key_gather_kernel(
       if (vsh) vsh[(size_t)(b + i + u) * 64 + l] = vv[u];
       v0 += T::to_f((uint16_t)(vv[u] & 0xffff));
       v1 += T::to_f((uint16_t)(vv[u] >> 16));
-      ax += xv[u];
+      ax0 += h2f((uint16_t)(xv[u] & 0xffff));
+      ax1 += h2f((uint16_t)(xv[u] >> 16));
     }
   }
   float* vo = vsum + ((size_t)h * C + c) * 128 + 2 * l;
@@ -397,9 +400,10 @@ __global__ __launch_bounds__(256) void key_gather_kernel(
   // the cluster's largest |value sum|, for the per-head scale lam
   const float mx = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
   if (l == 0) cmax[(size_t)h * C + c] = mx;
-  if (ck2 && l < 32) {
-    const size_t o = ((size_t)h * C + c) * KM_R + l;
-    ck2[o] = n ? ax / (float)n : h2f(ck0[o]);
+  if (ck2 && l < 16) {
+    const size_t o = ((size_t)h * C + c) * KM_R + 2 * l;
+    ck2[o] = n ? ax0 / (float)n : h2f(ck0[o]);
+    ck2[o + 1] = n ? ax1 / (float)n : h2f(ck0[o + 1]);
   }
 }
 
