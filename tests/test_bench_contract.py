@@ -1,8 +1,11 @@
-"""bench.py's command-line contract that holds without a GPU: one GPU only."""
+"""bench.py's command-line contract: one GPU only (CPU), and the whole bench
+path on a small config (GPU)."""
 import json
 import subprocess
 import sys
 from pathlib import Path
+
+import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
 
@@ -13,3 +16,21 @@ def test_more_than_one_gpu_exits_with_a_message():
     assert r.returncode != 0
     msg = json.loads(r.stdout.strip().splitlines()[-1])
     assert "one GPU" in msg["error"]
+
+
+@pytest.mark.gpu
+def test_bench_line_on_the_gpu():
+    """The whole bench path on a small config, dense leg included: one JSON
+    line with the contract's keys and a roofline for the exact kernel."""
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--config", "cpu_plumbing",
+                        "--steps", "2", "--warmup", "1", "--no-cpu-baseline"], cwd=ROOT,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
+                "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config",
+                "roofline", "cpu_baseline"):
+        assert key in d, key
+    assert d["n_gpus"] == 1 and d["steps"] == 2 and d["value"] > 0
+    assert d["roofline"]["bound"] == "mfma" and 0 < d["roofline"]["frac"] < 1
+    assert d["dense_tile_kernel_ms"] > 0
