@@ -4,14 +4,16 @@
 // Exact attention (one work-group per task of <= 128 sorted queries of one
 // query cluster, 4 waves x 32 queries, two work-groups per CU):
 //   * the union is turned into runs of cluster-ordered key rows in LDS, and
-//     the kp/vp rows of every 64-key tile are derived from them in parallel;
+//     the vp rows of every 64-key tile are derived from them in parallel (K
+//     rows through kperm, or from the cluster-ordered kp);
 //   * K and V tiles are gathered by LDS DMA into a double-buffered ring, row
 //     major with an XOR swizzle; tile t is consumed while tile t+1 is in
 //     flight, one barrier per tile;
 //   * S^T = K Q^T and O^T = V^T P^T on MFMA, so every lane owns one query: the
 //     online-softmax max/sum need one cross-half exchange, and the per-query
-//     rescale of O touches only the lane's own registers; V^T operands come
-//     from transposing LDS reads;
+//     rescale of O touches only the lane's own registers; the score chains
+//     read K four steps ahead, and V^T operands come from transposing LDS
+//     reads issued in inline assembly one dim block ahead;
 //   * the running max advances with a margin, so O is rescaled only when a
 //     tile raises the max by more than the margin.
 // Residual + merge (a separate kernel, one work-group per 128 consecutive
