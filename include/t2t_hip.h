@@ -211,6 +211,41 @@ int t2t_tile_attn_exact_orig_gather(const void* q, const void* k, const int32_t*
                                     const void* vp, int dtype, const int32_t* kcounts,
                                     const int32_t* unip, const int32_t* qperm, const int32_t* plan,
                                     void* out, float* lse, int H, int N, int CQ, void* stream);
+/* ---- strided variants ---------------------------------------------------
+ * No counterpart in the reference: its SGLang backend copies q, k and v from
+ * the model's token-major [1, N, H, 128] into head-major [H, N, 128] and the
+ * output back (integrations/sglang/backend/t2t_attn.py:1161-1163,1194), four
+ * full-size copies per call.  These entry points take the caller's tensors as
+ * [H, N, 128] views: row n of head h at base + h * head_stride + n * row_stride
+ * (elements; both multiples of 8, row stride >= 128, unit stride along the
+ * 128 dims), so a token-major tensor is passed as (head_stride, row_stride) =
+ * (128, H * 128).  Results are identical to the contiguous entry points. */
+int t2t_project_strided(const void* x, int x_dtype, const void* U, void* out, int H, int N, int D,
+                        int r, long long x_head_stride, long long x_row_stride, void* stream);
+int t2t_kmm_run_strided(const void* QU, const void* KU, const void* V, int v_dtype,
+                        long long v_head_stride, long long v_row_stride, const void* cq0,
+                        const void* ck0, int32_t* qlab, void* cq2, int32_t* klab, float* ck2,
+                        int32_t* qcounts, int32_t* qperm, int32_t* kcounts, int32_t* kperm,
+                        void* V_sorted, void* sumv, float* lam, int H, int N, int CQ, int CK,
+                        int pin_tail, void* ws, size_t ws_bytes, void* stream);
+int t2t_kmm_run_vstats_gather_strided(const void* V, int v_dtype, long long v_head_stride,
+                                      long long v_row_stride, const int32_t* kperm,
+                                      const int32_t* kcounts, void* V_sorted, void* sumv,
+                                      float* lam, int H, int N, int CK, void* ws,
+                                      size_t ws_bytes, void* stream);
+int t2t_tile_attn_exact_orig_gather_strided(
+    const void* q, long long q_head_stride, long long q_row_stride, const void* k,
+    long long k_head_stride, long long k_row_stride, const int32_t* kperm, const void* vp,
+    int dtype, const int32_t* kcounts, const int32_t* unip, const int32_t* qperm,
+    const int32_t* plan, void* out, long long out_head_stride, long long out_row_stride,
+    float* lse, int H, int N, int CQ, void* stream);
+int t2t_resid_merge_inplace_strided(void* out, long long out_head_stride, long long out_row_stride,
+                                    const float* lse, const void* QU, const void* tiles,
+                                    const int32_t* kcounts, const int32_t* unip,
+                                    const int32_t* qlab, const int32_t* qperm, const float* lam,
+                                    const float* tailw_dev, int dtype, int H, int N, int CQ,
+                                    void* stream);
+
 /* Residual + merge into the exact part held at the original rows of out
  * (S6); tiles from t2t_centroid_tiles.  With the two entries above, the
  * steps of t2t_tile_attn_run_planned one launch at a time. */

@@ -131,6 +131,44 @@ def test_fused_k_gather_is_bit_identical(dev, dtype):
     assert torch.equal(outs[True][1], outs[False][1])
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_token_major_views_are_bit_identical(dev, dtype):
+    """q, k, v given as token-major [N, H, 128] tensors seen through
+    .transpose(0, 1), with the output written into a token-major view: the
+    kernels read and write the rows in place (strided entry points) and give
+    the same bits as contiguous head-major inputs, on a full and a reuse call."""
+    deploy, q, k, v = make(dev, mask_refresh=4)
+    H, N = deploy.H, deploy.N
+    tq, tk, tv = (torch.from_numpy(a).to(dev).to(dtype) for a in (q, k, v))
+    state = deploy.init_state(tq, tk, seed=4)
+    tm = [t.transpose(0, 1).contiguous() for t in (tq, tk, tv)]  # [N, H, 128]
+    views = [t.transpose(0, 1) for t in tm]
+    assert not views[0].is_contiguous()
+    res = {}
+    for mode in ("contiguous", "token_major"):
+        st = {k_: v_.clone() for k_, v_ in state.items()}
+        deploy.reset_cfg_reuse()
+        outs = []
+        for parity in (0, 1):
+            deploy.set_cfg_call(parity, key=1, step=0)
+            if mode == "contiguous":
+                outs.append(deploy.step(tq, tk, tv, st).clone())
+            else:
+                o = torch.full((N, H, 128), float("nan"), device=dev, dtype=dtype)
+                r = deploy.step(*views, st, out=o.transpose(0, 1))
+                assert r.data_ptr() == o.data_ptr()
+                outs.append(o.transpose(0, 1).clone())
+            assert deploy.last_call_full == (parity == 0)
+        res[mode] = outs
+    for a_, b_ in zip(res["contiguous"], res["token_major"]):
+        assert torch.equal(a_, b_)
+    # the unfused path needs contiguous tensors and says so
+    deploy.fuse_k_gather = False
+    with pytest.raises(ValueError, match="fuse_k_gather"):
+        deploy.step(*views, state)
+    deploy.fuse_k_gather = True
+
+
 def test_bad_inputs_raise(dev):
     from token2tile_amd.deploy_step import MaskedStepDeploy
     with pytest.raises(ValueError):

@@ -9,7 +9,7 @@ arguments.
 from __future__ import annotations
 
 import ctypes
-from ctypes import c_float, c_int, c_size_t, c_void_p
+from ctypes import c_float, c_int, c_longlong, c_size_t, c_void_p
 from pathlib import Path
 
 import torch
@@ -53,6 +53,18 @@ SIGNATURES = {
                                          c_int, _P]),
     "t2t_tile_attn_exact_orig_gather": (c_int, [_P, _P, _P, _P, c_int, _P, _P, _P, _P, _P, _P,
                                                 c_int, c_int, c_int, _P]),
+    "t2t_project_strided": (c_int, [_P, c_int, _P, _P, c_int, c_int, c_int, c_int, c_longlong,
+                                    c_longlong, _P]),
+    "t2t_kmm_run_strided": (c_int, [_P, _P, _P, c_int, c_longlong, c_longlong] + [_P] * 13 +
+                            [c_int] * 5 + [_P, c_size_t, _P]),
+    "t2t_kmm_run_vstats_gather_strided": (c_int, [_P, c_int, c_longlong, c_longlong, _P, _P, _P,
+                                                  _P, _P, c_int, c_int, c_int, _P, c_size_t, _P]),
+    "t2t_tile_attn_exact_orig_gather_strided": (c_int, [_P, c_longlong, c_longlong, _P, c_longlong,
+                                                        c_longlong, _P, _P, c_int, _P, _P, _P, _P,
+                                                        _P, c_longlong, c_longlong, _P, c_int,
+                                                        c_int, c_int, _P]),
+    "t2t_resid_merge_inplace_strided": (c_int, [_P, c_longlong, c_longlong] + [_P] * 9 +
+                                        [c_int] * 4 + [_P]),
     "t2t_resid_merge_inplace": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int,
                                         c_int, c_int, _P]),
     "t2t_tail_merge_ws_bytes": (c_size_t, [c_int]),
@@ -89,10 +101,22 @@ def lib():
     return _lib
 
 
+class RowView:
+    """A strided tensor whose geometry the caller has validated and whose
+    strides it passes to a ``*_strided`` entry point beside the pointer."""
+    __slots__ = ("t",)
+
+    def __init__(self, t):
+        self.t = t
+
+
 def ptr(t):
-    """Device pointer of a tensor (None -> NULL)."""
+    """Device pointer of a tensor (None -> NULL).  Plain tensors must be
+    contiguous; a RowView passes its (validated) strided tensor's pointer."""
     if t is None:
         return None
+    if isinstance(t, RowView):
+        return t.t.data_ptr()
     if not isinstance(t, torch.Tensor):
         return t
     if not t.is_contiguous():
@@ -116,7 +140,7 @@ def stream_handle(stream=None):
 def call(name, *args):
     """Call a status-returning entry point; raise RuntimeError on failure."""
     fn = getattr(lib(), name)
-    rc = fn(*[ptr(a) if isinstance(a, torch.Tensor) else a for a in args])
+    rc = fn(*[ptr(a) if isinstance(a, (torch.Tensor, RowView)) else a for a in args])
     if rc != 0:
         msg = lib().t2t_last_error().decode(errors="replace")
         raise RuntimeError(f"{name} failed (code {rc}): {msg}")

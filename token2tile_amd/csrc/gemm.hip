@@ -12,7 +12,8 @@
 template <typename T, int D>
 __global__ __launch_bounds__(256) void project_kernel(const uint16_t* __restrict__ x,
                                                       const uint16_t* __restrict__ U,
-                                                      uint16_t* __restrict__ out, int N) {
+                                                      uint16_t* __restrict__ out, int N,
+                                                      long long sxh, long long sxn) {
   constexpr int KS = D / 16;
   const int h = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -28,7 +29,9 @@ __global__ __launch_bounds__(256) void project_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int t = 0; t < 4; ++t) ua[s][t] = (uint32_t)v[2 * t] | ((uint32_t)v[2 * t + 1] << 16);
   }
-  const uint16_t* xh = x + (size_t)h * N * D;
+  // x row n of head h at x + h sxh + n sxn (elements): [H, N, D] contiguous
+  // or a strided view such as the token-major [N, H, D]
+  const uint16_t* xh = x + (size_t)h * sxh;
   uint16_t* oh = out + (size_t)h * N * 32;
   for (int r0 = (blockIdx.x * 4 + wave) * 32; r0 < N; r0 += gridDim.x * 4 * 32) {
     const int row = r0 + jl;
@@ -37,7 +40,7 @@ __global__ __launch_bounds__(256) void project_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       u32x4 b = {0u, 0u, 0u, 0u};
-      if (ok) b = *(const u32x4*)(xh + (size_t)row * D + 16 * s + 8 * hh);
+      if (ok) b = *(const u32x4*)(xh + (size_t)row * sxn + 16 * s + 8 * hh);
       if constexpr (T::code == T2T_BF16) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -61,22 +64,22 @@ __global__ __launch_bounds__(256) void project_kernel(const uint16_t* __restrict
 
 template <typename T>
 static int launch_project(const void* x, const void* U, void* out, int H, int N, int D,
-                          hipStream_t st) {
+                          long long sxh, long long sxn, hipStream_t st) {
   int gx = cdiv(N, 128);
   if (gx > 1024) gx = 1024;
   dim3 grid(gx, H);
   switch (D) {
     case 128:
       hipLaunchKernelGGL((project_kernel<T, 128>), grid, dim3(256), 0, st, (const uint16_t*)x,
-                         (const uint16_t*)U, (uint16_t*)out, N);
+                         (const uint16_t*)U, (uint16_t*)out, N, sxh, sxn);
       break;
     case 64:
       hipLaunchKernelGGL((project_kernel<T, 64>), grid, dim3(256), 0, st, (const uint16_t*)x,
-                         (const uint16_t*)U, (uint16_t*)out, N);
+                         (const uint16_t*)U, (uint16_t*)out, N, sxh, sxn);
       break;
     case 32:
       hipLaunchKernelGGL((project_kernel<T, 32>), grid, dim3(256), 0, st, (const uint16_t*)x,
-                         (const uint16_t*)U, (uint16_t*)out, N);
+                         (const uint16_t*)U, (uint16_t*)out, N, sxh, sxn);
       break;
     default:
       t2t_set_error("project: D=%d not in {32, 64, 128}", D);
@@ -86,15 +89,30 @@ static int launch_project(const void* x, const void* U, void* out, int H, int N,
   return T2T_OK;
 }
 
-extern "C" int t2t_project(const void* x, int x_dtype, const void* U, void* out, int H, int N,
-                           int D, int r, void* stream) {
+static int project_impl(const void* x, int x_dtype, const void* U, void* out, int H, int N, int D,
+                        int r, long long sxh, long long sxn, void* stream) {
   T2T_REQUIRE(x && U && out, "project: null pointer");
   T2T_REQUIRE(H > 0 && N > 0, "project: H=%d N=%d", H, N);
   T2T_REQUIRE(r == 32, "project: rank r=%d (kernels are built for r=32)", r);
-  if (x_dtype == T2T_F16) return launch_project<F16T>(x, U, out, H, N, D, (hipStream_t)stream);
-  if (x_dtype == T2T_BF16) return launch_project<BF16T>(x, U, out, H, N, D, (hipStream_t)stream);
+  T2T_REQUIRE(sxn >= D && sxn % 8 == 0 && sxh % 8 == 0 && sxh >= 0,
+              "project: strides (%lld, %lld) must be multiples of 8 with row stride >= D", sxh, sxn);
+  if (x_dtype == T2T_F16)
+    return launch_project<F16T>(x, U, out, H, N, D, sxh, sxn, (hipStream_t)stream);
+  if (x_dtype == T2T_BF16)
+    return launch_project<BF16T>(x, U, out, H, N, D, sxh, sxn, (hipStream_t)stream);
   t2t_set_error("project: dtype %d", x_dtype);
   return T2T_ERR_ARG;
+}
+
+extern "C" int t2t_project(const void* x, int x_dtype, const void* U, void* out, int H, int N,
+                           int D, int r, void* stream) {
+  return project_impl(x, x_dtype, U, out, H, N, D, r, (long long)N * D, D, stream);
+}
+
+extern "C" int t2t_project_strided(const void* x, int x_dtype, const void* U, void* out, int H,
+                                   int N, int D, int r, long long x_head_stride,
+                                   long long x_row_stride, void* stream) {
+  return project_impl(x, x_dtype, U, out, H, N, D, r, x_head_stride, x_row_stride, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -359,7 +359,7 @@ __global__ __launch_bounds__(256) void key_gather_kernel(
     const int32_t* __restrict__ perm, const int32_t* __restrict__ counts,
     const int32_t* __restrict__ cbase, const uint16_t* __restrict__ ck0, float* __restrict__ ck2,
     uint16_t* __restrict__ V_sorted, float* __restrict__ vsum, float* __restrict__ cmax, int N,
-    int C) {
+    int C, long long svh, long long svn) {
   const int h = blockIdx.y;
   const int l = threadIdx.x & 63;
   const int c = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -368,7 +368,9 @@ __global__ __launch_bounds__(256) void key_gather_kernel(
   const int b = cbase[(size_t)h * C + c];
   const int32_t* ph = perm ? perm + (size_t)h * N + b : nullptr;
   const uint16_t* kh = KU ? KU + (size_t)h * N * KM_R : nullptr;
-  const uint32_t* vh = (const uint32_t*)(V + (size_t)h * N * 128);
+  // V row n of head h at V + h svh + n svn (elements; svn even)
+  const uint32_t* vh = (const uint32_t*)(V + (size_t)h * svh);
+  const size_t vrow = (size_t)(svn >> 1);
   uint32_t* vsh = V_sorted ? (uint32_t*)(V_sorted + (size_t)h * N * 128) : nullptr;
   // lanes 0..15 also sum the projected key rows, dims 2 l and 2 l + 1 (one
   // 4-byte load per row; each dim still sums its rows in order)
@@ -381,7 +383,7 @@ __global__ __launch_bounds__(256) void key_gather_kernel(
     for (int u = 0; u < KG_UNR; ++u) rw[u] = (i + u < n) ? (ph ? ph[i + u] : b + i + u) : -1;
 #pragma unroll
     for (int u = 0; u < KG_UNR; ++u) {
-      vv[u] = rw[u] >= 0 ? __builtin_nontemporal_load(&vh[(size_t)rw[u] * 64 + l]) : 0u;
+      vv[u] = rw[u] >= 0 ? __builtin_nontemporal_load(&vh[(size_t)rw[u] * vrow + l]) : 0u;
       xv[u] = (kh32 && rw[u] >= 0 && l < 16) ? kh32[(size_t)rw[u] * (KM_R / 2) + l] : 0u;
     }
 #pragma unroll
@@ -521,10 +523,10 @@ template <typename T>
 static void launch_key_gather(const void* KU, const void* V, const int32_t* perm,
                               const int32_t* counts, const int32_t* cbase, const void* ck0,
                               float* ck2, void* V_sorted, float* vsum, float* cmax, int H, int N,
-                              int C, hipStream_t st) {
+                              int C, long long svh, long long svn, hipStream_t st) {
   hipLaunchKernelGGL(key_gather_kernel<T>, dim3(cdiv(C, 4), H), dim3(256), 0, st,
                      (const uint16_t*)KU, (const uint16_t*)V, perm, counts, cbase,
-                     (const uint16_t*)ck0, ck2, (uint16_t*)V_sorted, vsum, cmax, N, C);
+                     (const uint16_t*)ck0, ck2, (uint16_t*)V_sorted, vsum, cmax, N, C, svh, svn);
 }
 
 #define KM_CHECK(x)            \
@@ -533,12 +535,12 @@ static void launch_key_gather(const void* KU, const void* V, const int32_t* perm
     if (_rc) return _rc;       \
   } while (0)
 
-extern "C" int t2t_kmm_run(const void* QU, const void* KU, const void* V, int v_dtype,
-                           const void* cq0, const void* ck0, int32_t* qlab, void* cq2,
-                           int32_t* klab, float* ck2, int32_t* qcounts, int32_t* qperm,
-                           int32_t* kcounts, int32_t* kperm, void* V_sorted, void* sumv,
-                           float* lam, int H, int N, int CQ, int CK, int pin_tail, void* ws,
-                           size_t ws_bytes, void* stream) {
+static int kmm_impl(const void* QU, const void* KU, const void* V, int v_dtype,
+                    const void* cq0, const void* ck0, int32_t* qlab, void* cq2, int32_t* klab,
+                    float* ck2, int32_t* qcounts, int32_t* qperm, int32_t* kcounts,
+                    int32_t* kperm, void* V_sorted, void* sumv, float* lam, int H, int N, int CQ,
+                    int CK, int pin_tail, void* ws, size_t ws_bytes, long long svh,
+                    long long svn, void* stream) {
   T2T_REQUIRE(QU && KU && V && cq0 && ck0 && qlab && cq2 && klab && ck2 && qcounts && qperm &&
                   kcounts && kperm && V_sorted && sumv && lam,
               "kmm_run: null pointer");
@@ -547,6 +549,8 @@ extern "C" int t2t_kmm_run(const void* QU, const void* KU, const void* V, int v_
   T2T_REQUIRE(CQ >= 1 && CQ <= KM_MAXC && CK >= 1 && CK <= KM_MAXC,
               "kmm_run: CQ=%d CK=%d must be in [1, %d]", CQ, CK, KM_MAXC);
   T2T_REQUIRE(pin_tail >= 0 && pin_tail <= N, "kmm_run: pin_tail must be in [0, N]");
+  T2T_REQUIRE(svn >= 128 && svn % 8 == 0 && svh >= 0 && svh % 8 == 0,
+              "kmm_run: V strides (%lld, %lld) must be multiples of 8, row stride >= 128", svh, svn);
   const KmmWs need = kmm_layout(H, N, CQ, CK, nullptr);
   if (!ws || ws_bytes < need.total) {
     t2t_set_error("kmm_run: workspace %zu < %zu bytes", ws_bytes, need.total);
@@ -575,14 +579,37 @@ extern "C" int t2t_kmm_run(const void* QU, const void* KU, const void* V, int v_
   KM_CHECK(run_sort(klab, kcounts, w.cbasek, kperm, w.chist, H, N, CK, st));
   if (v_dtype == T2T_F16)
     launch_key_gather<F16T>(KU, V, kperm, kcounts, w.cbasek, ck0, ck2, V_sorted, w.vsum, w.cmax, H, N, CK,
-                            st);
+                            svh, svn, st);
   else
     launch_key_gather<BF16T>(KU, V, kperm, kcounts, w.cbasek, ck0, ck2, V_sorted, w.vsum, w.cmax, H, N, CK,
-                             st);
+                             svh, svn, st);
   T2T_LAUNCH_CHECK("key gather");
   launch_vstats(w.vsum, w.cmax, sumv, lam, H, CK, st);
   T2T_LAUNCH_CHECK("vstats");
   return T2T_OK;
+}
+
+extern "C" int t2t_kmm_run(const void* QU, const void* KU, const void* V, int v_dtype,
+                           const void* cq0, const void* ck0, int32_t* qlab, void* cq2,
+                           int32_t* klab, float* ck2, int32_t* qcounts, int32_t* qperm,
+                           int32_t* kcounts, int32_t* kperm, void* V_sorted, void* sumv,
+                           float* lam, int H, int N, int CQ, int CK, int pin_tail, void* ws,
+                           size_t ws_bytes, void* stream) {
+  return kmm_impl(QU, KU, V, v_dtype, cq0, ck0, qlab, cq2, klab, ck2, qcounts, qperm, kcounts,
+                  kperm, V_sorted, sumv, lam, H, N, CQ, CK, pin_tail, ws, ws_bytes,
+                  (long long)N * 128, 128, stream);
+}
+
+extern "C" int t2t_kmm_run_strided(const void* QU, const void* KU, const void* V, int v_dtype,
+                                   long long v_head_stride, long long v_row_stride,
+                                   const void* cq0, const void* ck0, int32_t* qlab, void* cq2,
+                                   int32_t* klab, float* ck2, int32_t* qcounts, int32_t* qperm,
+                                   int32_t* kcounts, int32_t* kperm, void* V_sorted, void* sumv,
+                                   float* lam, int H, int N, int CQ, int CK, int pin_tail,
+                                   void* ws, size_t ws_bytes, void* stream) {
+  return kmm_impl(QU, KU, V, v_dtype, cq0, ck0, qlab, cq2, klab, ck2, qcounts, qperm, kcounts,
+                  kperm, V_sorted, sumv, lam, H, N, CQ, CK, pin_tail, ws, ws_bytes, v_head_stride,
+                  v_row_stride, stream);
 }
 
 // ---- value statistics of a reuse call ----
@@ -633,10 +660,12 @@ extern "C" size_t t2t_vstats_ws_bytes(int H, int N, int CK) {
 
 static int vstats_common(const void* V, int v_dtype, const int32_t* kperm, const int32_t* kcounts,
                          void* V_sorted, void* sumv, float* lam, int H, int N, int CK, void* ws,
-                         size_t ws_bytes, hipStream_t st) {
+                         size_t ws_bytes, long long svh, long long svn, hipStream_t st) {
   T2T_REQUIRE(V && kcounts && sumv && lam, "vstats: null pointer");
   T2T_REQUIRE(v_dtype == T2T_F16 || v_dtype == T2T_BF16, "vstats: dtype %d", v_dtype);
   T2T_REQUIRE(H > 0 && N > 0 && CK >= 1 && CK <= KM_MAXC, "vstats: H=%d N=%d CK=%d", H, N, CK);
+  T2T_REQUIRE(svn >= 128 && svn % 8 == 0 && svh >= 0 && svh % 8 == 0,
+              "vstats: V strides (%lld, %lld) must be multiples of 8, row stride >= 128", svh, svn);
   const size_t need = vws_layout(H, CK, nullptr).total;
   if (!ws || ws_bytes < need) {
     t2t_set_error("vstats: workspace %zu < %zu bytes", ws_bytes, need);
@@ -646,10 +675,10 @@ static int vstats_common(const void* V, int v_dtype, const int32_t* kperm, const
   hipLaunchKernelGGL(cbase_kernel, dim3(H), dim3(1024), 0, st, kcounts, w.cbase, CK);
   if (v_dtype == T2T_F16)
     launch_key_gather<F16T>(nullptr, V, kperm, kcounts, w.cbase, nullptr, nullptr, V_sorted,
-                            w.vsum, w.cmax, H, N, CK, st);
+                            w.vsum, w.cmax, H, N, CK, svh, svn, st);
   else
     launch_key_gather<BF16T>(nullptr, V, kperm, kcounts, w.cbase, nullptr, nullptr, V_sorted,
-                             w.vsum, w.cmax, H, N, CK, st);
+                             w.vsum, w.cmax, H, N, CK, svh, svn, st);
   launch_vstats(w.vsum, w.cmax, sumv, lam, H, CK, st);
   T2T_LAUNCH_CHECK("vstats");
   return T2T_OK;
@@ -661,14 +690,25 @@ extern "C" int t2t_kmm_run_vstats_gather(const void* V, int v_dtype, const int32
                                          size_t ws_bytes, void* stream) {
   T2T_REQUIRE(kperm && V_sorted, "vstats_gather: null kperm / V_sorted");
   return vstats_common(V, v_dtype, kperm, kcounts, V_sorted, sumv, lam, H, N, CK, ws, ws_bytes,
-                       (hipStream_t)stream);
+                       (long long)N * 128, 128, (hipStream_t)stream);
+}
+
+extern "C" int t2t_kmm_run_vstats_gather_strided(const void* V, int v_dtype,
+                                                 long long v_head_stride, long long v_row_stride,
+                                                 const int32_t* kperm, const int32_t* kcounts,
+                                                 void* V_sorted, void* sumv, float* lam, int H,
+                                                 int N, int CK, void* ws, size_t ws_bytes,
+                                                 void* stream) {
+  T2T_REQUIRE(kperm && V_sorted, "vstats_gather: null kperm / V_sorted");
+  return vstats_common(V, v_dtype, kperm, kcounts, V_sorted, sumv, lam, H, N, CK, ws, ws_bytes,
+                       v_head_stride, v_row_stride, (hipStream_t)stream);
 }
 
 extern "C" int t2t_kmm_run_vstats(const void* V_sorted, int v_dtype, const int32_t* kcounts,
                                   void* sumv, float* lam, int H, int N, int CK, void* ws,
                                   size_t ws_bytes, void* stream) {
   return vstats_common(V_sorted, v_dtype, nullptr, kcounts, nullptr, sumv, lam, H, N, CK, ws,
-                       ws_bytes, (hipStream_t)stream);
+                       ws_bytes, (long long)N * 128, 128, (hipStream_t)stream);
 }
 
 // ---------------------------------------------------------------------------

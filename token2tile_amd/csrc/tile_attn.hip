@@ -278,7 +278,10 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     const int32_t* __restrict__ qperm, const int32_t* __restrict__ kcounts,
     const int32_t* __restrict__ k_off, const int32_t* __restrict__ ntask,
     const int32_t* __restrict__ tasks, uint16_t* __restrict__ attn_out, float* __restrict__ lse,
-    uint16_t* __restrict__ out, const int32_t* __restrict__ kperm, int H, int N, int CQ, int maxT) {
+    uint16_t* __restrict__ out, const int32_t* __restrict__ kperm, int H, int N, int CQ, int maxT,
+    long long sqh, long long sqn, long long skh, long long skn, long long soh, long long son) {
+  // row n of head h of q / k (MODE 2) / out (MODE 1, 2) sits at base + h s_h + n s_n
+  // (elements): [H, N, 128] contiguous or a strided view such as token-major [N, H, 128]
   constexpr bool KG = MODE == 2;
   // two separate arrays (not one [2][...] array): the K DMA into one buffer
   // must not be taken as a possible writer of the other one, or every read of
@@ -440,11 +443,14 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     // ---- queries: B operand fragments (dims 16 s + 8 hh .. + 7)
     u32x4 qb[8];
     {
-      const uint16_t* qr = q + ((size_t)h * N + orig) * TA_D + 8 * hh;
+      const uint16_t* qr = q + (size_t)h * sqh + (size_t)orig * sqn + 8 * hh;
 #pragma unroll
       for (int s = 0; s < 8; ++s) qb[s] = *(const u32x4*)(qr + 16 * s);
     }
-    const char* kh = (const char*)(kp + (size_t)h * N * TA_D);
+    const char* kh = (const char*)(kp + (KG ? (size_t)h * skh : (size_t)h * N * TA_D));
+    // byte offsets of K rows from the head base stay 32-bit (the entry point
+    // checks (N - 1) * row stride fits): 64-bit address math here cost 3.6%
+    const uint32_t krow_bytes = KG ? (uint32_t)(skn * 2) : 256u;
     const char* vh = (const char*)(vp + (size_t)h * N * TA_D);
     const int ntile = (kvlen + TA_KT - 1) / TA_KT;
     // source rows of tile `tile` -> sIdx[tile & 1]; past the end -> row 0
@@ -504,7 +510,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
         const int blk = 4 * i + wave;
         const int row = 4 * blk + (lane >> 4);
         const uint32_t base = (uint32_t)sIdx[buf][row] * 256u;
-        const uint32_t kbase = KG ? (uint32_t)sIdxK[buf][row] * 256u : base;
+        const uint32_t kbase = KG ? (uint32_t)sIdxK[buf][row] * krow_bytes : base;
         const uint32_t offk = kbase + 16u * ((lane & 15) ^ (row & 15));
         const uint32_t offv = base + 16u * ((lane & 15) ^ sv_swz(row));
         __builtin_amdgcn_global_load_lds((const glb_void_t*)(kh + offk),
@@ -633,7 +639,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
   // kernel, the original row of out, read back by the merge
   if (qok) {
     uint16_t* orow =
-        MODE != 0 ? out + ((size_t)h * N + orig) * TA_D : attn_out + (obase + qrow) * TA_D;
+        MODE != 0 ? out + (size_t)h * soh + (size_t)orig * son : attn_out + (obase + qrow) * TA_D;
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
@@ -649,13 +655,20 @@ template <typename T, int MODE>
 static void launch_attn(const void* q, const void* kp, const void* vp, const int32_t* unip,
                         const int32_t* qperm, const int32_t* kcounts, const PlanView& p,
                         void* attn_out, float* lse, void* out, int H, int N, int CQ,
-                        hipStream_t st, const int32_t* kperm = nullptr) {
+                        hipStream_t st, const int32_t* kperm = nullptr, long long sqh = -1,
+                        long long sqn = TA_D, long long skh = -1, long long skn = TA_D,
+                        long long soh = -1, long long son = TA_D) {
+  // default strides: [H, N, 128] contiguous
+  if (sqh < 0) sqh = (long long)N * TA_D;
+  if (skh < 0) skh = (long long)N * TA_D;
+  if (soh < 0) soh = (long long)N * TA_D;
   const int total = H * p.maxT;
   const int grid = ((total + 63) / 64) * 64;
   hipLaunchKernelGGL((attn_kernel<T, MODE>), dim3(grid), dim3(TA_WAVES * 64), 0, st,
                      (const uint16_t*)q, (const uint16_t*)kp, (const uint16_t*)vp,
                      (const uint32_t*)unip, qperm, kcounts, p.k_off, p.ntask, p.tasks,
-                     (uint16_t*)attn_out, lse, (uint16_t*)out, kperm, H, N, CQ, p.maxT);
+                     (uint16_t*)attn_out, lse, (uint16_t*)out, kperm, H, N, CQ, p.maxT, sqh, sqn,
+                     skh, skn, soh, son);
 }
 
 // ---------------------------------------------------------------------------
@@ -710,7 +723,7 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
     const int32_t* __restrict__ kcounts, const uint32_t* __restrict__ unip,
     const int32_t* __restrict__ qlab, const int32_t* __restrict__ qperm,
     const float* __restrict__ lam, const float* __restrict__ tailw, uint16_t* __restrict__ out,
-    int N, int CQ) {
+    int N, int CQ, long long soh, long long son) {
   __shared__ __attribute__((aligned(1024))) uint16_t sT0[RT_HALVES];
   __shared__ __attribute__((aligned(1024))) uint16_t sT1[RT_HALVES];
   // counts as fp16, ordered so that the 16 a lane weights in one 32-centroid
@@ -874,9 +887,9 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
   const bool bad = ph <= 1.0e-6f * ex;
   const float den = fmaxf(ex + ph * tw, 1.0e-12f);
   const float wx = ex / den, wt = st * tw * lm / den;
-  const uint16_t* er = SRC_SORTED ? exact + ((size_t)h * N + row) * TA_D
-                                  : out + ((size_t)h * N + orig) * TA_D;
-  uint16_t* orow = out + ((size_t)h * N + orig) * TA_D;
+  // out row n of head h at out + h soh + n son (elements)
+  uint16_t* orow = out + (size_t)h * soh + (size_t)orig * son;
+  const uint16_t* er = SRC_SORTED ? exact + ((size_t)h * N + row) * TA_D : orow;
   if (bad && !SRC_SORTED) return;  // the exact part in out is the output
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb)
@@ -929,18 +942,20 @@ template <bool SRC_SORTED>
 static void launch_resid(int dtype, const void* exact, const float* lse, const void* QU,
                          const void* tiles, const int32_t* kcounts, const int32_t* unip,
                          const int32_t* qlab, const int32_t* qperm, const float* lam,
-                         const float* tailw, void* out, int H, int N, int CQ, hipStream_t st) {
+                         const float* tailw, void* out, int H, int N, int CQ, hipStream_t st,
+                         long long soh = -1, long long son = TA_D) {
   const dim3 grid(cdiv(N, 128), H);
+  if (soh < 0) soh = (long long)N * TA_D;
   if (dtype == T2T_F16)
     hipLaunchKernelGGL((resid_kernel<F16T, SRC_SORTED>), grid, dim3(256), 0, st,
                        (const uint16_t*)exact, lse, (const uint16_t*)QU, (const uint16_t*)tiles,
                        kcounts, (const uint32_t*)unip, qlab, qperm, lam, tailw, (uint16_t*)out, N,
-                       CQ);
+                       CQ, soh, son);
   else
     hipLaunchKernelGGL((resid_kernel<BF16T, SRC_SORTED>), grid, dim3(256), 0, st,
                        (const uint16_t*)exact, lse, (const uint16_t*)QU, (const uint16_t*)tiles,
                        kcounts, (const uint32_t*)unip, qlab, qperm, lam, tailw, (uint16_t*)out, N,
-                       CQ);
+                       CQ, soh, son);
 }
 
 extern "C" size_t t2t_tail_merge_ws_bytes(int H) { return t2t_centroid_tiles_bytes(H); }
@@ -977,24 +992,55 @@ extern "C" int t2t_centroid_tiles(const void* cks, const void* sumv, void* tiles
   return T2T_OK;
 }
 
-extern "C" int t2t_tile_attn_exact_orig_gather(const void* q, const void* k, const int32_t* kperm,
-                                               const void* vp, int dtype, const int32_t* kcounts,
-                                               const int32_t* unip, const int32_t* qperm,
-                                               const int32_t* plan, void* out, float* lse, int H,
-                                               int N, int CQ, void* stream) {
+static int exact_gather_impl(const void* q, long long sqh, long long sqn, const void* k,
+                             long long skh, long long skn, const int32_t* kperm, const void* vp,
+                             int dtype, const int32_t* kcounts, const int32_t* unip,
+                             const int32_t* qperm, const int32_t* plan, void* out, long long soh,
+                             long long son, float* lse, int H, int N, int CQ, void* stream) {
   T2T_REQUIRE(q && k && kperm && vp && kcounts && unip && qperm && plan && out && lse,
               "tile_attn_exact_orig_gather: null pointer");
   T2T_REQUIRE(check_dtype(dtype), "tile_attn_exact_orig_gather: dtype %d", dtype);
   T2T_REQUIRE(H > 0 && N > 0 && N < (1 << 24) && CQ > 0,
               "tile_attn_exact_orig_gather: H=%d N=%d CQ=%d", H, N, CQ);
+  T2T_REQUIRE(sqn >= TA_D && skn >= TA_D && son >= TA_D && sqn % 8 == 0 && skn % 8 == 0 &&
+                  son % 8 == 0 && sqh >= 0 && skh >= 0 && soh >= 0 && sqh % 8 == 0 &&
+                  skh % 8 == 0 && soh % 8 == 0,
+              "tile_attn_exact_orig_gather: strides must be non-negative multiples of 8 elements "
+              "with row strides >= 128");
+  T2T_REQUIRE((unsigned long long)(N - 1) * (unsigned long long)skn * 2ull + 256ull <= 0xFFFFFFFFull,
+              "tile_attn_exact_orig_gather: one head's K rows span (N - 1) * %lld elements, more "
+              "than 4 GiB", skn);
   PlanView p = plan_view((int32_t*)plan, H, N, CQ);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == T2T_F16)
-    launch_attn<F16T, 2>(q, k, vp, unip, qperm, kcounts, p, nullptr, lse, out, H, N, CQ, st, kperm);
+    launch_attn<F16T, 2>(q, k, vp, unip, qperm, kcounts, p, nullptr, lse, out, H, N, CQ, st, kperm,
+                         sqh, sqn, skh, skn, soh, son);
   else
-    launch_attn<BF16T, 2>(q, k, vp, unip, qperm, kcounts, p, nullptr, lse, out, H, N, CQ, st, kperm);
+    launch_attn<BF16T, 2>(q, k, vp, unip, qperm, kcounts, p, nullptr, lse, out, H, N, CQ, st, kperm,
+                          sqh, sqn, skh, skn, soh, son);
   T2T_LAUNCH_CHECK("tile_attn_exact_orig_gather");
   return T2T_OK;
+}
+
+extern "C" int t2t_tile_attn_exact_orig_gather(const void* q, const void* k, const int32_t* kperm,
+                                               const void* vp, int dtype, const int32_t* kcounts,
+                                               const int32_t* unip, const int32_t* qperm,
+                                               const int32_t* plan, void* out, float* lse, int H,
+                                               int N, int CQ, void* stream) {
+  const long long hs = (long long)N * TA_D;
+  return exact_gather_impl(q, hs, TA_D, k, hs, TA_D, kperm, vp, dtype, kcounts, unip, qperm, plan,
+                           out, hs, TA_D, lse, H, N, CQ, stream);
+}
+
+extern "C" int t2t_tile_attn_exact_orig_gather_strided(
+    const void* q, long long q_head_stride, long long q_row_stride, const void* k,
+    long long k_head_stride, long long k_row_stride, const int32_t* kperm, const void* vp,
+    int dtype, const int32_t* kcounts, const int32_t* unip, const int32_t* qperm,
+    const int32_t* plan, void* out, long long out_head_stride, long long out_row_stride,
+    float* lse, int H, int N, int CQ, void* stream) {
+  return exact_gather_impl(q, q_head_stride, q_row_stride, k, k_head_stride, k_row_stride, kperm,
+                           vp, dtype, kcounts, unip, qperm, plan, out, out_head_stride,
+                           out_row_stride, lse, H, N, CQ, stream);
 }
 
 extern "C" int t2t_tile_attn_exact_orig(const void* q, const void* kp, const void* vp, int dtype,
@@ -1016,20 +1062,42 @@ extern "C" int t2t_tile_attn_exact_orig(const void* q, const void* kp, const voi
   return T2T_OK;
 }
 
+static int resid_inplace_impl(void* out, long long soh, long long son, const float* lse,
+                              const void* QU, const void* tiles, const int32_t* kcounts,
+                              const int32_t* unip, const int32_t* qlab, const int32_t* qperm,
+                              const float* lam, const float* tailw_dev, int dtype, int H, int N,
+                              int CQ, void* stream) {
+  T2T_REQUIRE(out && lse && QU && tiles && kcounts && unip && qlab && qperm && lam && tailw_dev,
+              "resid_merge_inplace: null pointer");
+  T2T_REQUIRE(check_dtype(dtype), "resid_merge_inplace: dtype %d", dtype);
+  T2T_REQUIRE(H > 0 && N > 0 && CQ > 0, "resid_merge_inplace: H=%d N=%d CQ=%d", H, N, CQ);
+  T2T_REQUIRE(son >= TA_D && son % 8 == 0 && soh >= 0 && soh % 8 == 0,
+              "resid_merge_inplace: out strides (%lld, %lld)", soh, son);
+  launch_resid<false>(dtype, nullptr, lse, QU, tiles, kcounts, unip, qlab, qperm, lam, tailw_dev,
+                      out, H, N, CQ, (hipStream_t)stream, soh, son);
+  T2T_LAUNCH_CHECK("resid_merge_inplace");
+  return T2T_OK;
+}
+
 extern "C" int t2t_resid_merge_inplace(void* out, const float* lse, const void* QU,
                                        const void* tiles, const int32_t* kcounts,
                                        const int32_t* unip, const int32_t* qlab,
                                        const int32_t* qperm, const float* lam,
                                        const float* tailw_dev, int dtype, int H, int N, int CQ,
                                        void* stream) {
-  T2T_REQUIRE(out && lse && QU && tiles && kcounts && unip && qlab && qperm && lam && tailw_dev,
-              "resid_merge_inplace: null pointer");
-  T2T_REQUIRE(check_dtype(dtype), "resid_merge_inplace: dtype %d", dtype);
-  T2T_REQUIRE(H > 0 && N > 0 && CQ > 0, "resid_merge_inplace: H=%d N=%d CQ=%d", H, N, CQ);
-  launch_resid<false>(dtype, nullptr, lse, QU, tiles, kcounts, unip, qlab, qperm, lam, tailw_dev,
-                      out, H, N, CQ, (hipStream_t)stream);
-  T2T_LAUNCH_CHECK("resid_merge_inplace");
-  return T2T_OK;
+  return resid_inplace_impl(out, (long long)N * TA_D, TA_D, lse, QU, tiles, kcounts, unip, qlab,
+                            qperm, lam, tailw_dev, dtype, H, N, CQ, stream);
+}
+
+extern "C" int t2t_resid_merge_inplace_strided(void* out, long long out_head_stride,
+                                               long long out_row_stride, const float* lse,
+                                               const void* QU, const void* tiles,
+                                               const int32_t* kcounts, const int32_t* unip,
+                                               const int32_t* qlab, const int32_t* qperm,
+                                               const float* lam, const float* tailw_dev,
+                                               int dtype, int H, int N, int CQ, void* stream) {
+  return resid_inplace_impl(out, out_head_stride, out_row_stride, lse, QU, tiles, kcounts, unip,
+                            qlab, qperm, lam, tailw_dev, dtype, H, N, CQ, stream);
 }
 
 extern "C" size_t t2t_tile_attn_ws_bytes(int H, int N, int dtype) {

@@ -279,18 +279,26 @@ class MaskedStepDeploy:
         self._cfg_parity = None
 
     # -- the attention call (deploy_step.py:286-477) -------------------------
-    def step(self, q, k, v, state):
-        """q, k, v: [H, N, 128] fp16 (or bf16) contiguous, original row order.
+    def step(self, q, k, v, state, out=None):
+        """q, k, v: [H, N, 128] fp16 (or bf16), original row order: contiguous,
+        or strided views with contiguous rows, such as token-major [N, H, 128]
+        tensors through ``.transpose(0, 1)`` (the kernels read them in place).
         state: dict(Uq, Uk, ck, cq) fp16; ck/cq are replaced by fresh tensors
         holding the centroids that warm-start the next call.  Returns out
-        [H, N, 128] in q's dtype (a buffer reused by the next call)."""
+        [H, N, 128] in q's dtype: the given ``out`` view (written in place), or
+        a buffer reused by the next call."""
         H, N, C, CQ, D = self.H, self.N, self.C, self.CQ, self.D
-        for name, t in (("q", q), ("k", k), ("v", v)):
-            if tuple(t.shape) != (H, N, D) or not t.is_contiguous() or t.device != self.dev:
-                raise ValueError(f"step: {name} must be a contiguous [{H}, {N}, {D}] tensor on "
-                                 f"{self.dev}")
         if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.float16, torch.bfloat16):
             raise TypeError("step: q, k, v must share dtype fp16 or bf16")
+        for name, t in (("q", q), ("k", k), ("v", v)) + ((("out", out),) if out is not None else ()):
+            try:
+                ops._rows(t, H, N, D, q.dtype, name, self.dev)
+            except ValueError as e:
+                raise ValueError(f"step: {e}") from None
+        if not self.fuse_k_gather and not (q.is_contiguous() and k.is_contiguous()
+                                           and (out is None or out.is_contiguous())):
+            raise ValueError("step: strided q, k or out need fuse_k_gather (the separate gather "
+                             "path reads and writes contiguous tensors)")
         # the kernels take raw pointers: a state of the wrong geometry would be
         # read out of bounds, so it is checked here
         for name, shape in (("Uq", (H, D, self.r)), ("Uk", (H, D, self.r)), ("ck", (H, C, self.r)),
@@ -305,6 +313,7 @@ class MaskedStepDeploy:
         if caller != s0:
             s0.wait_stream(caller)
         io = self._buffers(q.dtype)
+        dst = io["out"] if out is None else out
 
         snap = None
         held = None
@@ -409,14 +418,14 @@ class MaskedStepDeploy:
             with self._stage("attention_exact"):
                 if self.fuse_k_gather:
                     ops.tile_attn_exact_orig_gather(q, k, kperm, io["vp"], counts, unip, qperm, plan,
-                                                    io["out"], self._lse, stream=s0)
+                                                    dst, self._lse, stream=s0)
                 else:
                     ops.tile_attn_exact_orig(q, io["kp"], io["vp"], counts, unip, qperm, plan,
-                                             io["out"], self._lse, stream=s0)
+                                             dst, self._lse, stream=s0)
             if qu_ready is not None:
                 s0.wait_event(qu_ready)
             with self._stage("attention_residual"):
-                ops.resid_merge_inplace(io["out"], self._lse, self.QU, self._ctiles, counts, unip,
+                ops.resid_merge_inplace(dst, self._lse, self.QU, self._ctiles, counts, unip,
                                         qlab_cur, qperm, self._kmm_lam, self.tailw_t, stream=s0)
         s1.wait_stream(s0)
         cur = torch.cuda.current_stream(self.dev)
@@ -424,4 +433,4 @@ class MaskedStepDeploy:
         cur.wait_stream(s1)
         self._last = dict(unip=unip, qperm=qperm, tile_sizes=tile_sizes, counts=counts,
                           qlab=qlab_cur, cks=cks, plan=plan, kperm=kperm)
-        return io["out"]
+        return dst

@@ -59,6 +59,24 @@ def _check(t, shape, dtype, name, device=None):
                          f"{tuple(t.shape)} on {t.device}")
 
 
+def _rows(t, H, N, D, dtype, name, device):
+    """Validate an [H, N, D] view whose rows are contiguous (unit stride along
+    D, 16-byte aligned) and return its (head, row) strides in elements: the
+    contiguous layout, or e.g. a token-major [N, H, D] tensor seen through
+    ``.transpose(0, 1)``."""
+    dtypes = dtype if isinstance(dtype, tuple) else (dtype,)
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"t2t: {name} must be a tensor")
+    sh, sn = (t.stride(0), t.stride(1)) if t.dim() == 3 else (0, 0)
+    if (tuple(t.shape) != (H, N, D) or t.dtype not in dtypes or t.device != device
+            or t.stride(2) != 1 or sh % 8 or sn % 8 or sn < D or sh < 0
+            or t.data_ptr() % 16):
+        raise ValueError(f"t2t: {name} must be a {'/'.join(map(str, dtypes))} [{H}, {N}, {D}] "
+                         f"tensor on {device} with contiguous 16-byte aligned rows, got "
+                         f"{t.dtype} {tuple(t.shape)} strides {tuple(t.stride())} on {t.device}")
+    return sh, sn
+
+
 def _check_ns(ns_t, device):
     if not isinstance(ns_t, torch.Tensor) or ns_t.numel() != 1 or ns_t.dtype != _i32 \
             or ns_t.device != device:
@@ -76,11 +94,16 @@ def project(x, U, out=None, stream=None):
     """fp16(x @ U): x [H, N, D] fp16/bf16, U [H, D, 32] fp16 -> [H, N, 32] fp16."""
     H, N, D = x.shape
     dev = _dev(x)
-    _check(x, (H, N, D), _HALF, "x", dev)
+    sxh, sxn = _rows(x, H, N, D, _HALF, "x", dev)
     _check(U, (H, D, RANK), _f16, "U", dev)
     if out is None:
         out = torch.empty(H, N, RANK, dtype=_f16, device=dev)
     _check(out, (H, N, RANK), _f16, "out", dev)
+    if not x.is_contiguous():
+        call("t2t_project_strided", _lib.RowView(x), dtype_code(x.dtype), U, out, H, N, D, RANK,
+             sxh, sxn,
+             stream_handle(stream))
+        return out
     call("t2t_project", x, dtype_code(x.dtype), U, out, H, N, D, RANK, stream_handle(stream))
     return out
 
@@ -98,7 +121,7 @@ def kmm_run(QU, KU, V, cq0, ck0, *, pin_tail=0, out=None, ws=None, stream=None):
     _check(KU, (H, N, r), _f16, "KU", dev)
     _check(cq0, (H, CQ, r), _f16, "cq0", dev)
     _check(ck0, (H, CK, r), _f16, "ck0", dev)
-    _check(V, (H, N, HEAD_DIM), _HALF, "V", dev)
+    svh, svn = _rows(V, H, N, HEAD_DIM, _HALF, "V", dev)
     o = dict(out or {})
     o.setdefault("qlab", torch.empty(H, N, dtype=_i32, device=dev))
     o.setdefault("cq2", torch.empty(H, CQ, r, dtype=_f16, device=dev))
@@ -108,7 +131,7 @@ def kmm_run(QU, KU, V, cq0, ck0, *, pin_tail=0, out=None, ws=None, stream=None):
     o.setdefault("qperm", torch.empty(H, N, dtype=_i32, device=dev))
     o.setdefault("kcounts", torch.empty(H, CK, dtype=_i32, device=dev))
     o.setdefault("kperm", torch.empty(H, N, dtype=_i32, device=dev))
-    o.setdefault("V_sorted", torch.empty_like(V))
+    o.setdefault("V_sorted", torch.empty(H, N, HEAD_DIM, dtype=V.dtype, device=dev))
     o.setdefault("sumv", torch.empty(H, CK, HEAD_DIM, dtype=_f16, device=dev))
     o.setdefault("lam", torch.empty(H, dtype=_f32, device=dev))
     for name, shape, dt in (("qlab", (H, N), _i32), ("cq2", (H, CQ, r), _f16),
@@ -120,9 +143,17 @@ def kmm_run(QU, KU, V, cq0, ck0, *, pin_tail=0, out=None, ws=None, stream=None):
         _check(o[name], shape, dt, name, dev)
     need = kmm_ws_bytes(H, N, CQ, CK)
     ws = _ws_for(ws, need, dev)
-    call("t2t_kmm_run", QU, KU, V, dtype_code(V.dtype), cq0, ck0, o["qlab"], o["cq2"], o["klab"],
-         o["ck2"], o["qcounts"], o["qperm"], o["kcounts"], o["kperm"], o["V_sorted"], o["sumv"],
-         o["lam"], H, N, CQ, CK, int(pin_tail), ws, ws.numel(), stream_handle(stream))
+    if V.is_contiguous():
+        call("t2t_kmm_run", QU, KU, V, dtype_code(V.dtype), cq0, ck0, o["qlab"], o["cq2"],
+             o["klab"], o["ck2"], o["qcounts"], o["qperm"], o["kcounts"], o["kperm"],
+             o["V_sorted"], o["sumv"], o["lam"], H, N, CQ, CK, int(pin_tail), ws, ws.numel(),
+             stream_handle(stream))
+    else:
+        call("t2t_kmm_run_strided", QU, KU, _lib.RowView(V), dtype_code(V.dtype), svh, svn, cq0,
+             ck0, o["qlab"],
+             o["cq2"], o["klab"], o["ck2"], o["qcounts"], o["qperm"], o["kcounts"], o["kperm"],
+             o["V_sorted"], o["sumv"], o["lam"], H, N, CQ, CK, int(pin_tail), ws, ws.numel(),
+             stream_handle(stream))
     return o
 
 
@@ -135,10 +166,11 @@ def vstats_gather(V, kperm, kcounts, V_sorted=None, sumv=None, lam=None, ws=None
     H, N, D = V.shape
     CK = kcounts.shape[1]
     dev = _dev(V)
-    V_sorted = torch.empty_like(V) if V_sorted is None else V_sorted
+    V_sorted = (torch.empty(H, N, D, dtype=V.dtype, device=dev) if V_sorted is None
+                else V_sorted)
     sumv = torch.empty(H, CK, D, dtype=_f16, device=dev) if sumv is None else sumv
     lam = torch.empty(H, dtype=_f32, device=dev) if lam is None else lam
-    _check(V, (H, N, HEAD_DIM), _HALF, "V", dev)
+    svh, svn = _rows(V, H, N, HEAD_DIM, _HALF, "V", dev)
     _check(kperm, (H, N), _i32, "kperm", dev)
     _check(kcounts, (H, CK), _i32, "kcounts", dev)
     _check(V_sorted, (H, N, HEAD_DIM), V.dtype, "V_sorted", dev)
@@ -146,8 +178,13 @@ def vstats_gather(V, kperm, kcounts, V_sorted=None, sumv=None, lam=None, ws=None
     _check(lam, (H,), _f32, "lam", dev)
     need = vstats_ws_bytes(H, N, CK)
     ws = _ws_for(ws, need, dev)
-    call("t2t_kmm_run_vstats_gather", V, dtype_code(V.dtype), kperm, kcounts, V_sorted, sumv, lam,
-         H, N, CK, ws, ws.numel(), stream_handle(stream))
+    if V.is_contiguous():
+        call("t2t_kmm_run_vstats_gather", V, dtype_code(V.dtype), kperm, kcounts, V_sorted, sumv,
+             lam, H, N, CK, ws, ws.numel(), stream_handle(stream))
+    else:
+        call("t2t_kmm_run_vstats_gather_strided", _lib.RowView(V), dtype_code(V.dtype), svh, svn,
+             kperm, kcounts,
+             V_sorted, sumv, lam, H, N, CK, ws, ws.numel(), stream_handle(stream))
     return V_sorted, sumv, lam
 
 
@@ -401,27 +438,44 @@ def tile_attn_exact_orig(q, kp, vp, kcounts, unip, qperm, plan, out, lse, stream
 
 def tile_attn_exact_orig_gather(q, k, kperm, vp, kcounts, unip, qperm, plan, out, lse, stream=None):
     """tile_attn_exact_orig reading K in place: k in the original order, key
-    position p of the cluster order at row kperm[h, p] (no kp = k[kperm])."""
+    position p of the cluster order at row kperm[h, p] (no kp = k[kperm]).
+    q, k and out may be strided [H, N, 128] views with contiguous rows (e.g.
+    token-major tensors through ``.transpose(0, 1)``)."""
     H, N, D = q.shape
     CQ = unip.shape[1]
     dev = _dev(q)
-    _check_attn(dev, H, N, CQ, q=q, kp=k, vp=vp, kcounts=kcounts, unip=unip, qperm=qperm,
-                plan=plan, out=out, lse=lse, dt=q.dtype)
+    sq = _rows(q, H, N, HEAD_DIM, _HALF, "q", dev)
+    sk = _rows(k, H, N, HEAD_DIM, q.dtype, "k", dev)
+    so = _rows(out, H, N, HEAD_DIM, q.dtype, "out", dev)
+    _check_attn(dev, H, N, CQ, vp=vp, kcounts=kcounts, unip=unip, qperm=qperm, plan=plan,
+                lse=lse, dt=q.dtype)
     _check(kperm, (H, N), _i32, "kperm", dev)
-    call("t2t_tile_attn_exact_orig_gather", q, k, kperm, vp, dtype_code(q.dtype), kcounts, unip,
-         qperm, plan, out, lse, H, N, CQ, stream_handle(stream))
+    if q.is_contiguous() and k.is_contiguous() and out.is_contiguous():
+        call("t2t_tile_attn_exact_orig_gather", q, k, kperm, vp, dtype_code(q.dtype), kcounts,
+             unip, qperm, plan, out, lse, H, N, CQ, stream_handle(stream))
+    else:
+        call("t2t_tile_attn_exact_orig_gather_strided", _lib.RowView(q), *sq, _lib.RowView(k),
+             *sk, kperm, vp, dtype_code(q.dtype), kcounts, unip, qperm, plan, _lib.RowView(out),
+             *so, lse, H, N, CQ, stream_handle(stream))
     return out
-
 
 def resid_merge_inplace(out, lse, QU, tiles, kcounts, unip, qlab, qperm, lam, tailw_t,
                         stream=None):
-    """Residual + merge into the exact part held at the original rows of out."""
+    """Residual + merge into the exact part held at the original rows of out
+    (out may be a strided [H, N, 128] view with contiguous rows)."""
     H, N, D = out.shape
     CQ = unip.shape[1]
-    _check_attn(_dev(out), H, N, CQ, q=out, lse=lse, QU=QU, tiles=tiles, kcounts=kcounts,
-                unip=unip, qlab=qlab, qperm=qperm, lam=lam, tailw_t=tailw_t)
-    call("t2t_resid_merge_inplace", out, lse, QU, tiles, kcounts, unip, qlab, qperm, lam, tailw_t,
-         dtype_code(out.dtype), H, N, CQ, stream_handle(stream))
+    dev = _dev(out)
+    so = _rows(out, H, N, HEAD_DIM, _HALF, "out", dev)
+    _check_attn(dev, H, N, CQ, lse=lse, QU=QU, tiles=tiles, kcounts=kcounts, unip=unip,
+                qlab=qlab, qperm=qperm, lam=lam, tailw_t=tailw_t)
+    if out.is_contiguous():
+        call("t2t_resid_merge_inplace", out, lse, QU, tiles, kcounts, unip, qlab, qperm, lam,
+             tailw_t, dtype_code(out.dtype), H, N, CQ, stream_handle(stream))
+    else:
+        call("t2t_resid_merge_inplace_strided", _lib.RowView(out), *so, lse, QU, tiles, kcounts,
+             unip, qlab,
+             qperm, lam, tailw_t, dtype_code(out.dtype), H, N, CQ, stream_handle(stream))
     return out
 
 
