@@ -289,8 +289,12 @@ int t2t_det_centroid_update(const void* x, const int32_t* labels, const void* ol
                             void* ws, size_t ws_bytes, void* stream);
 /* G[h] = x[h]^T x[h] / N in fp64 ([H, D, D]); bf16 x is rounded to fp16
  * first.  Replaces the Gram products of online_u,
- * operator/deploy_step.py:135-137. D <= 128. */
-int t2t_gram(const void* x, int x_dtype, double* G, int H, int N, int D, void* stream);
+ * operator/deploy_step.py:135-137. D <= 128.  ws holds the per-split partial
+ * products (t2t_gram_ws_bytes); the splits are summed in a fixed order, so the
+ * result is the same on every call. */
+size_t t2t_gram_ws_bytes(int H, int N, int D);
+int t2t_gram(const void* x, int x_dtype, double* G, int H, int N, int D, void* ws,
+             size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

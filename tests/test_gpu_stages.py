@@ -487,3 +487,22 @@ def test_wrappers_reject_mismatched_tensors(dev):
             f()
             pytest.fail(f"case {i} was accepted")
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("N,D", [(5003, 128), (777, 96), (64, 128)])
+def test_gram_full_width(dev, dtype, N, D):
+    """fp64 Gram on MFMA at the operator's width: the split partial sums add
+    up to x^T x / N (products of fp16 values are exact in fp64)."""
+    from token2tile_amd import ops
+    rng = np.random.default_rng(N + D)
+    x = rng.normal(0, 1, (3, N, D)).astype(np.float16)
+    xt = g(x, dev)
+    if dtype == "bf16":
+        xt = xt.to(torch.bfloat16)
+        x = xt.float().cpu().numpy().astype(np.float16)   # bf16 is rounded to fp16 first
+    G = c(ops.gram(xt))
+    xd = x.astype(np.float64)
+    ref = np.einsum("hni,hnj->hij", xd, xd) / N
+    assert np.allclose(G, ref, rtol=1e-12, atol=1e-12)
+    assert np.array_equal(G, c(ops.gram(xt)))              # same result on every call

@@ -205,82 +205,131 @@ extern "C" int t2t_score(const void* QU, const void* cks, void* gl, int H, int N
 // sum runs over rows in order, so the result is deterministic).
 // grid (tiles, H); each work-group owns a 64 x 64 output tile.
 // ---------------------------------------------------------------------------
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+#define GR_ROWS 64      // rows staged per step
+#define GR_MAXSPLIT 64  // row splits per head (partial Grams in the workspace)
+
+// Partial Gram products on fp64 MFMA (v_mfma_f64_16x16x4_f64).  Block (s, h)
+// sums rows [s R, s R + R) of head h; wave w owns the 64 x 64 quadrant
+// (w / 2, w % 2) of the D x D result as 4 x 4 blocks of 16 x 16.  Rows are
+// staged through LDS as fp32 (exact for fp16 values; bf16 is rounded to fp16
+// first, as the reference's backend casts to fp16).  For a k-step of four
+// rows, lane l holds x[n + l / 16][c + l % 16] as both the A (Xt, 16 x 4)
+// and the B (X, 4 x 16) fragment of column block c, and the 16 x 16 result
+// block keeps G[c_i + l / 16 + 4 r][c_j + l % 16] in register r of lane l
+// (rows interleaved by four, as measured on the GPU).
+// Products of fp16 values are exact in fp64, and each output sums its rows in
+// a fixed order, so the result does not depend on the launch.
 template <typename T>
 __global__ __launch_bounds__(256) void gram_kernel(const uint16_t* __restrict__ x,
-                                                   double* __restrict__ G, int N, int D) {
-  __shared__ float sA[64][65];
-  __shared__ float sB[64][65];
-  const int h = blockIdx.y;
-  const int tiles = (D + 63) / 64;
-  const int ti = blockIdx.x / tiles, tj = blockIdx.x % tiles;
-  const int tid = threadIdx.x;
-  const int oi = (tid / 16) * 4, oj = (tid % 16) * 4;  // 4 x 4 outputs per thread
-  double acc[4][4];
+                                                   double* __restrict__ part, int N, int D, int R) {
+  __shared__ float sx[GR_ROWS][128 + 4];
+  const int s = blockIdx.x, h = blockIdx.y, H = gridDim.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int qi = w >> 1, qj = w & 1;
+  const bool act = qi * 64 < D && qj * 64 < D;
+  const int r0 = s * R;
+  const int r1 = r0 + R < N ? r0 + R : N;
+  f64x4 acc[4][4];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) acc[a][b] = 0.0;
+    for (int j = 0; j < 4; ++j) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
   const uint16_t* xh = x + (size_t)h * N * D;
-  for (int n0 = 0; n0 < N; n0 += 64) {
+  const int kr = lane >> 4, kc = lane & 15;
+  for (int n0 = r0; n0 < r1; n0 += GR_ROWS) {
     __syncthreads();
-    for (int i = tid; i < 64 * 64; i += 256) {
-      const int rr = i / 64, cc = i % 64;
+    for (int i = tid; i < GR_ROWS * 128; i += 256) {
+      const int rr = i >> 7, cc = i & 127;
       const int n = n0 + rr;
-      float va = 0.f, vb = 0.f;
-      if (n < N) {
-        const int ca = ti * 64 + cc, cb = tj * 64 + cc;
-        if (ca < D) {
-          uint16_t u = xh[(size_t)n * D + ca];
-          va = (T::code == T2T_BF16) ? h2f(bf2h(u)) : h2f(u);
-        }
-        if (cb < D) {
-          uint16_t u = xh[(size_t)n * D + cb];
-          vb = (T::code == T2T_BF16) ? h2f(bf2h(u)) : h2f(u);
-        }
+      float v = 0.f;
+      if (n < r1 && cc < D) {
+        const uint16_t u = xh[(size_t)n * D + cc];
+        v = (T::code == T2T_BF16) ? h2f(bf2h(u)) : h2f(u);
       }
-      sA[rr][cc] = va;
-      sB[rr][cc] = vb;
+      sx[rr][cc] = v;
     }
     __syncthreads();
-    const int nr = (N - n0) < 64 ? (N - n0) : 64;
-    for (int rr = 0; rr < nr; ++rr) {
-      double a[4], b[4];
+    if (act) {
+#pragma unroll 2
+      for (int k = 0; k < GR_ROWS; k += 4) {
+        double a[4], b[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        a[t] = (double)sA[rr][oi + t];
-        b[t] = (double)sB[rr][oj + t];
+        for (int t = 0; t < 4; ++t) {
+          a[t] = (double)sx[k + kr][64 * qi + 16 * t + kc];
+          b[t] = (double)sx[k + kr][64 * qj + 16 * t + kc];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[i][j], 0, 0, 0);
       }
-#pragma unroll
-      for (int p = 0; p < 4; ++p)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc[p][q] = __fma_rn(a[p], b[q], acc[p][q]);
     }
   }
-  const double inv = 1.0 / (double)N;
+  if (!act) return;
+  double* ph = part + ((size_t)s * H + h) * D * D;
 #pragma unroll
-  for (int p = 0; p < 4; ++p)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int i = ti * 64 + oi + p, j = tj * 64 + oj + q;
-      if (i < D && j < D) G[((size_t)h * D + i) * D + j] = acc[p][q] * inv;
-    }
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int gi = 64 * qi + 16 * i + kr + 4 * r, gj = 64 * qj + 16 * j + kc;
+        if (gi < D && gj < D) ph[(size_t)gi * D + gj] = acc[i][j][r];
+      }
 }
 
-extern "C" int t2t_gram(const void* x, int x_dtype, double* G, int H, int N, int D, void* stream) {
+// G[h] = (sum over the splits, in split order, of the partial Grams) / N
+__global__ __launch_bounds__(256) void gram_reduce_kernel(const double* __restrict__ part,
+                                                          double* __restrict__ G, int S, int H,
+                                                          int N, int D) {
+  const int h = blockIdx.y;
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= D * D) return;
+  double acc = 0.0;
+  for (int s = 0; s < S; ++s) acc += part[((size_t)s * H + h) * D * D + e];
+  G[(size_t)h * D * D + e] = acc / (double)N;
+}
+
+static int gram_splits(int H, int N) {
+  int S = (1024 + H - 1) / H;  // about 1024 work-groups
+  const int maxS = (N + 4 * GR_ROWS - 1) / (4 * GR_ROWS);  // >= 4 staging steps per split
+  if (S > maxS) S = maxS;
+  if (S > GR_MAXSPLIT) S = GR_MAXSPLIT;
+  return S < 1 ? 1 : S;
+}
+
+extern "C" size_t t2t_gram_ws_bytes(int H, int N, int D) {
+  if (H <= 0 || N <= 0 || D <= 0) return 0;
+  return t2t_align256((size_t)gram_splits(H, N) * H * D * D * sizeof(double));
+}
+
+extern "C" int t2t_gram(const void* x, int x_dtype, double* G, int H, int N, int D, void* ws,
+                        size_t ws_bytes, void* stream) {
   T2T_REQUIRE(x && G, "gram: null pointer");
   T2T_REQUIRE(H > 0 && N > 0 && D > 0 && D <= 128, "gram: H=%d N=%d D=%d", H, N, D);
-  const int tiles = (D + 63) / 64;
-  dim3 grid(tiles * tiles, H);
+  const size_t need = t2t_gram_ws_bytes(H, N, D);
+  if (!ws || ws_bytes < need) {
+    t2t_set_error("gram: workspace %zu < %zu bytes", ws_bytes, need);
+    return T2T_ERR_WORKSPACE;
+  }
+  const int S = gram_splits(H, N);
+  const int R = ((N + S - 1) / S + 3) / 4 * 4;
+  hipStream_t st = (hipStream_t)stream;
+  double* part = (double*)ws;
   if (x_dtype == T2T_F16)
-    hipLaunchKernelGGL(gram_kernel<F16T>, grid, dim3(256), 0, (hipStream_t)stream,
-                       (const uint16_t*)x, G, N, D);
+    hipLaunchKernelGGL(gram_kernel<F16T>, dim3(S, H), dim3(256), 0, st, (const uint16_t*)x, part,
+                       N, D, R);
   else if (x_dtype == T2T_BF16)
-    hipLaunchKernelGGL(gram_kernel<BF16T>, grid, dim3(256), 0, (hipStream_t)stream,
-                       (const uint16_t*)x, G, N, D);
+    hipLaunchKernelGGL(gram_kernel<BF16T>, dim3(S, H), dim3(256), 0, st, (const uint16_t*)x, part,
+                       N, D, R);
   else {
     t2t_set_error("gram: dtype %d", x_dtype);
     return T2T_ERR_ARG;
   }
+  hipLaunchKernelGGL(gram_reduce_kernel, dim3((D * D + 255) / 256, H), dim3(256), 0, st, part, G,
+                     S, H, N, D);
   T2T_LAUNCH_CHECK("gram");
   return T2T_OK;
 }

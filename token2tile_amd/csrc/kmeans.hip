@@ -376,26 +376,55 @@ __global__ __launch_bounds__(256) void key_gather_kernel(
   // 4-byte load per row; each dim still sums its rows in order)
   float ax0 = 0.f, ax1 = 0.f, v0 = 0.f, v1 = 0.f;
   const uint32_t* kh32 = (const uint32_t*)kh;
-  for (int i = 0; i < n; i += KG_UNR) {
-    int rw[KG_UNR];
-    uint32_t vv[KG_UNR], xv[KG_UNR];
+  // The cluster's row indices are read 64 at a time (one coalesced load) and
+  // taken lane by lane as wave-uniform values, so each row's loads address
+  // from a scalar base.  Rows go in chunks of KG_UNR, software pipelined:
+  // chunk i + 1's loads are in flight while chunk i is stored and summed.
+  // Every load is unconditional (rows past the block repeat its last row and
+  // are not consumed), so the memory-counter waits can count on them.
+  auto run = [&](auto KS) {
+    constexpr bool ks = decltype(KS)::value;
+    int nxt = (l < n) ? (ph ? ph[l] : b + l) : 0;
+    for (int i0 = 0; i0 < n; i0 += 64) {
+      const int myrow = nxt;
+      nxt = (i0 + 64 + l < n) ? (ph ? ph[i0 + 64 + l] : b + i0 + 64 + l) : 0;
+      const int m = n - i0 < 64 ? n - i0 : 64;
+      uint32_t va[2][KG_UNR], xa[2][KG_UNR];
+      auto load = [&](int i, uint32_t (&vv)[KG_UNR], uint32_t (&xv)[KG_UNR]) {
 #pragma unroll
-    for (int u = 0; u < KG_UNR; ++u) rw[u] = (i + u < n) ? (ph ? ph[i + u] : b + i + u) : -1;
+        for (int u = 0; u < KG_UNR; ++u) {
+          const int rw = __builtin_amdgcn_readlane(myrow, i + u < m ? i + u : m - 1);
+          vv[u] = __builtin_nontemporal_load(&vh[(size_t)rw * vrow + l]);
+          if constexpr (ks) xv[u] = kh32[(size_t)rw * (KM_R / 2) + (l & 15)];
+        }
+      };
+      auto consume = [&](int i, const uint32_t (&vv)[KG_UNR], const uint32_t (&xv)[KG_UNR]) {
 #pragma unroll
-    for (int u = 0; u < KG_UNR; ++u) {
-      vv[u] = rw[u] >= 0 ? __builtin_nontemporal_load(&vh[(size_t)rw[u] * vrow + l]) : 0u;
-      xv[u] = (kh32 && rw[u] >= 0 && l < 16) ? kh32[(size_t)rw[u] * (KM_R / 2) + l] : 0u;
+        for (int u = 0; u < KG_UNR; ++u) {
+          if (i + u >= m) break;
+          if (vsh) vsh[(size_t)(b + i0 + i + u) * 64 + l] = vv[u];
+          v0 += T::to_f((uint16_t)(vv[u] & 0xffff));
+          v1 += T::to_f((uint16_t)(vv[u] >> 16));
+          if constexpr (ks) {
+            ax0 += h2f((uint16_t)(xv[u] & 0xffff));
+            ax1 += h2f((uint16_t)(xv[u] >> 16));
+          }
+        }
+      };
+      load(0, va[0], xa[0]);
+      for (int i = 0; i < m; i += 2 * KG_UNR) {
+        load(i + KG_UNR, va[1], xa[1]);
+        consume(i, va[0], xa[0]);
+        if (i + KG_UNR >= m) break;
+        if (i + 2 * KG_UNR < m) load(i + 2 * KG_UNR, va[0], xa[0]);
+        consume(i + KG_UNR, va[1], xa[1]);
+      }
     }
-#pragma unroll
-    for (int u = 0; u < KG_UNR; ++u) {
-      if (rw[u] < 0) break;
-      if (vsh) vsh[(size_t)(b + i + u) * 64 + l] = vv[u];
-      v0 += T::to_f((uint16_t)(vv[u] & 0xffff));
-      v1 += T::to_f((uint16_t)(vv[u] >> 16));
-      ax0 += h2f((uint16_t)(xv[u] & 0xffff));
-      ax1 += h2f((uint16_t)(xv[u] >> 16));
-    }
-  }
+  };
+  if (kh32)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
   float* vo = vsum + ((size_t)h * C + c) * 128 + 2 * l;
   vo[0] = v0;
   vo[1] = v1;
@@ -435,9 +464,16 @@ __global__ __launch_bounds__(1024) void vstats_kernel(const float* __restrict__ 
   const size_t i0 = ((size_t)blockIdx.x * 1024 + tid) * VS_PER;
   const float* vh = vsum + (size_t)h * CE;
   uint16_t* sh = sumv + (size_t)h * CE;
+  if (i0 + VS_PER <= CE) {  // CE is a multiple of 128: every group is whole
+    const f32x4 a = *(const f32x4*)(vh + i0), b = *(const f32x4*)(vh + i0 + 4);
+    u32x4 o;
 #pragma unroll
-  for (int e = 0; e < VS_PER; ++e)
-    if (i0 + e < CE) sh[i0 + e] = f2h(opaque(vh[i0 + e] * inv));
+    for (int e = 0; e < 2; ++e) {
+      o[e] = (uint32_t)f2h(opaque(a[2 * e] * inv)) | ((uint32_t)f2h(opaque(a[2 * e + 1] * inv)) << 16);
+      o[2 + e] = (uint32_t)f2h(opaque(b[2 * e] * inv)) | ((uint32_t)f2h(opaque(b[2 * e + 1] * inv)) << 16);
+    }
+    *(u32x4*)(sh + i0) = o;
+  }
 }
 static void launch_vstats(const float* vsum, const float* cmax, void* sumv, float* lam, int H,
                           int C, hipStream_t st) {

@@ -532,5 +532,7 @@ def gram(x, stream=None):
     H, N, D = x.shape
     _check(x, (H, N, D), _HALF, "x", _dev(x))
     G = torch.empty(H, D, D, dtype=torch.float64, device=_dev(x))
-    call("t2t_gram", x, dtype_code(x.dtype), G, H, N, D, stream_handle(stream))
+    nws = size_query("t2t_gram_ws_bytes", H, N, D)
+    ws = torch.empty(nws, dtype=torch.uint8, device=_dev(x))
+    call("t2t_gram", x, dtype_code(x.dtype), G, H, N, D, ws, nws, stream_handle(stream))
     return G
