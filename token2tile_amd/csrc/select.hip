@@ -166,31 +166,51 @@ __device__ inline uint32_t select_row(const int (&key)[32], const int (&sz)[32],
     *rowcnt = wgt + weq;
     return bits;
   }
-  const int R = ns - wgt;  // >= 1 keys still needed from the tied clusters
-  int before = 0;          // tied weight of all earlier chunks g
-  int took = 0;
+  // ---- several clusters on the key vstar: all keys above it are taken
+  //      (weight wgt < ns), then the tied clusters in ascending cluster order
+  //      (index 512 g + 8 lane + j) until their weight reaches R; the tied
+  //      cluster where it does is istar, and every tied cluster up to it is
+  //      taken, empty ones included
+  const int R = ns - wgt;  // >= 1
+  uint32_t gt = 0, tie = 0;
+#pragma unroll
+  for (int i = 31; i >= 0; --i) {
+    asm("v_cmp_gt_i32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
+        : "+v"(gt)
+        : "v"(key[i]), "v"(vstar)
+        : "vcc");
+    asm("v_cmp_eq_i32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
+        : "+v"(tie)
+        : "v"(key[i]), "v"(vstar)
+        : "vcc");
+  }
+  int cum = 0, istar = -1;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    int t = 0;
+    unsigned long long bal = __ballot(((tie >> (8 * g)) & 0xffu) != 0u);
+    while (bal != 0ull && istar < 0) {  // wave-uniform
+      const int L = (int)__ffsll((long long)bal) - 1;
+      bal &= bal - 1ull;
+      const uint32_t byte = ((uint32_t)__builtin_amdgcn_readlane((int)tie, L) >> (8 * g)) & 0xffu;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) t += (key[8 * g + j] == vstar) ? sz[8 * g + j] : 0;
-    const int inc = wave_incl_scan(t);
-    int p = before + inc - t;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = 8 * g + j;
-      bool s = key[i] > vstar;
-      if (key[i] == vstar) {
-        s = p < R;
-        if (s) took += sz[i];
-        p += sz[i];
+      for (int j = 0; j < 8; ++j) {
+        if (istar < 0 && ((byte >> j) & 1u)) {
+          cum += __builtin_amdgcn_readlane(sz[8 * g + j], L);
+          if (cum >= R) istar = 512 * g + 8 * L + j;
+        }
       }
-      bits |= (uint32_t)s << i;
     }
-    before += __builtin_amdgcn_readlane(inc, 63);
   }
-  *rowcnt = wgt + wave_sum(took);
-  return bits;
+  // tied keys of the lane with cluster index <= istar
+  uint32_t upto = 0;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    int w = istar - (512 * g + 8 * l) + 1;
+    w = w < 0 ? 0 : (w > 8 ? 8 : w);
+    upto |= ((1u << w) - 1u) << (8 * g);
+  }
+  *rowcnt = wgt + cum;
+  return gt | (tie & upto);
 }
 
 // publish the lanes' masks into the packed union row (LSB-first words);
