@@ -220,6 +220,9 @@ __device__ inline int xcd_remap(int bid, int total) {
 }
 
 #define TA_MARGIN 3.0f   // log2 units of headroom when the exact-part max advances
+// a tile is redone with a new max when one lane's weight sum passes this: far
+// inside the range of bf16 P (fp32 exponents), below fp16's largest value
+#define TA_WLIM (T::code == T2T_BF16 ? 0x1p64f : 0x1p14f)
 #define TL_MARGIN 2.0f   // natural-log units of headroom for the residual max
 #define TL_CT 64         // centroids per residual tile
 #define TL_CP 40         // residual centroid tile pitch (halves)
@@ -557,34 +560,44 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
           for (int a = 0; a < 16; ++a)
             if (32 * kb + 8 * (a / 4) + 4 * hh + (a % 4) >= valid) S[kb][a] = -__builtin_inff();
       }
-      float mr = -__builtin_inff();
+      // weights against the current m, without a per-tile max: exp2 scales
+      // exactly, so m only has to keep the weights in the range of T.  A tile
+      // whose weights leave it (the first one, m = -inf, or scores far above
+      // every earlier tile) is redone with m moved past its max, the sums so
+      // far rescaled (the reference's lazy max, taken only when needed)
+      u32x4 pb[4];
+      auto expo = [&](float nm) {
+        float acc = 0.f;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int a = 0; a < 16; a += 2) mr = vmax(mr, vmax(S[kb][a], S[kb][a + 1]));
-      mr = half_max(mr);
-      const float mx = mr * c;
-      // lazy max: move only when exceeded, then with headroom
-      if (__builtin_amdgcn_readfirstlane((int)(__ballot(mx > m) != 0ull))) {
+          for (int a = 0; a < 16; a += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(S[kb][a], c, nm));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(S[kb][a + 1], c, nm));
+            const uint32_t pk = Pk<T>::pack(p0, p1);
+            acc = Pk<T>::sum2(pk, acc);
+            pb[2 * kb + a / 8][(a % 8) / 2] = pk;
+          }
+        return acc;
+      };
+      float lt = expo(-m);
+      if (__builtin_amdgcn_readfirstlane((int)(__ballot(!(lt <= TA_WLIM)) != 0ull))) {
         T2T_REAL_BRANCH();
+        float mr = -__builtin_inff();
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int a = 0; a < 16; a += 2) mr = vmax(mr, vmax(S[kb][a], S[kb][a + 1]));
+        mr = half_max(mr);
+        const float mx = mr * c;
         const float mnew = mx > m ? mx + TA_MARGIN : m;
         const float alpha = __builtin_amdgcn_exp2f(m - mnew);
         m = mnew;
         lsum *= alpha;
         rescale(O, alpha);
+        lt = expo(-m);
       }
-      const float nm = -m;
-      u32x4 pb[4];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int a = 0; a < 16; a += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(S[kb][a], c, nm));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(S[kb][a + 1], c, nm));
-          const uint32_t pk = Pk<T>::pack(p0, p1);
-          lsum = Pk<T>::sum2(pk, lsum);
-          pb[2 * kb + a / 8][(a % 8) / 2] = pk;
-        }
+      lsum += lt;
       pv(O, buf ? sV1 : sV0, pb);
     };
     using B0 = std::integral_constant<int, 0>;
