@@ -820,17 +820,52 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
         mk[g + 4] = __builtin_amdgcn_perm(Y, X, 0x0b0b0909u);
       }
       f16x2 sp[8];
-      f16x2 mp = {(_Float16)-__builtin_inff(), (_Float16)-__builtin_inff()};
 #pragma unroll
       for (int a = 0; a < 16; a += 2) {
         const uint32_t pk = Pk<F16T>::pack(S[a], S[a + 1]);
         sp[a / 2] = __builtin_bit_cast(f16x2, bfi(mk[a / 2], 0xfc00fc00u, pk));
-        mp = __builtin_elementwise_maximum(mp, sp[a / 2]);
       }
-      float mx = vmax((float)mp[0], (float)mp[1]);
-      mx = half_max(mx);
-      if (__builtin_amdgcn_readfirstlane((int)(__ballot(mx > m2) != 0ull))) {
+      // weights against the current max, without taking this half's max: the
+      // exponentials scale exactly, so m2 only has to keep the fp16 P in
+      // range.  The count-weighted sum of the half bounds the weight of every
+      // cluster holding keys, and a weight that overflows to inf makes it inf
+      // or (count 0) NaN; a half whose sum is not <= 2^14 (the first one,
+      // m2 = -1e30, or scores far above the earlier ones) is redone with m2
+      // moved past its max (the reference's lazy max), the sums so far
+      // rescaled.  An empty cluster's weight can pass unseen only while finite.
+      u32x4 pb[2];
+      const u32x4* cw = (const u32x4*)(sCnt + TL_CT * tc + 32 * kb + 16 * hh);
+      const u32x4 cn0 = cw[0], cn1 = cw[1];
+      auto expo = [&](float nm) {
+        float ph = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float pe[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            pe[e] = __builtin_amdgcn_exp2f(fmaf((float)sp[2 * j + e / 2][e % 2], L2E, nm));
+          const uint32_t p01 = Pk<F16T>::pack(pe[0], pe[1]), p23 = Pk<F16T>::pack(pe[2], pe[3]);
+          pb[j / 2][2 * (j % 2)] = p01;
+          pb[j / 2][2 * (j % 2) + 1] = p23;
+          // (copied to scalars first: a bit_cast straight from a vector element
+          // reads element 0)
+          const uint32_t c01 = (j < 2 ? cn0 : cn1)[2 * (j % 2)];
+          const uint32_t c23 = (j < 2 ? cn0 : cn1)[2 * (j % 2) + 1];
+          ph = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p01), __builtin_bit_cast(f16x2, c01),
+                                      ph, false);
+          ph = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p23), __builtin_bit_cast(f16x2, c23),
+                                      ph, false);
+        }
+        return ph;
+      };
+      float pt = expo(-m2 * L2E);
+      if (__builtin_amdgcn_readfirstlane((int)(__ballot(!(pt <= 0x1p14f)) != 0ull))) {
         T2T_REAL_BRANCH();
+        f16x2 mp = {(_Float16)-__builtin_inff(), (_Float16)-__builtin_inff()};
+#pragma unroll
+        for (int a = 0; a < 8; ++a) mp = __builtin_elementwise_maximum(mp, sp[a]);
+        float mx = vmax((float)mp[0], (float)mp[1]);
+        mx = half_max(mx);
         const float mnew = mx > m2 ? mx + TL_MARGIN : m2;
         const float alpha = __builtin_amdgcn_exp2f((m2 - mnew) * L2E);
         m2 = mnew;
@@ -839,31 +874,9 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
         for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
           for (int a = 0; a < 16; ++a) O[nb][a] *= alpha;
+        pt = expo(-m2 * L2E);
       }
-      const float nm = -m2 * L2E;
-      // P as fp16 pairs; the count-weighted sum takes the same rounded P
-      // through v_dot2_f32_f16 (the counts are exact in fp16 up to 2048)
-      u32x4 pb[2];
-      const u32x4* cw = (const u32x4*)(sCnt + TL_CT * tc + 32 * kb + 16 * hh);
-      const u32x4 cn0 = cw[0], cn1 = cw[1];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float pe[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          pe[e] = __builtin_amdgcn_exp2f(fmaf((float)sp[2 * j + e / 2][e % 2], L2E, nm));
-        const uint32_t p01 = Pk<F16T>::pack(pe[0], pe[1]), p23 = Pk<F16T>::pack(pe[2], pe[3]);
-        pb[j / 2][2 * (j % 2)] = p01;
-        pb[j / 2][2 * (j % 2) + 1] = p23;
-        // (copied to scalars first: a bit_cast straight from a vector element
-        // reads element 0)
-        const uint32_t c01 = (j < 2 ? cn0 : cn1)[2 * (j % 2)];
-        const uint32_t c23 = (j < 2 ? cn0 : cn1)[2 * (j % 2) + 1];
-        phi = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p01), __builtin_bit_cast(f16x2, c01),
-                                     phi, false);
-        phi = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p23), __builtin_bit_cast(f16x2, c23),
-                                     phi, false);
-      }
+      phi += pt;
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
         const int dim = 32 * nb + jl;
