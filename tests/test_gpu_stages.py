@@ -6,6 +6,7 @@ the stated tolerances.  Each stage is fed the same inputs on both sides
 (the GPU's previous-stage outputs where a stage has an MMA-rounded input).
 """
 import math
+import zlib
 
 import numpy as np
 import pytest
@@ -117,7 +118,7 @@ def sel_inputs(rng, kind, H, N, CQ):
 @pytest.mark.parametrize("ns", [1, 300, 4096])
 def test_select_union_bit_exact(dev, kind, ns):
     from token2tile_amd import ops
-    rng = np.random.default_rng(hash((kind, ns)) % (2 ** 32))
+    rng = np.random.default_rng(zlib.crc32(f"select-{kind}-{ns}".encode()))
     H, N, CQ = 2, 4096, 24
     gl, sizes, qperm, qcounts = sel_inputs(rng, kind, H, N, CQ)
     ns_t = torch.tensor(ns, dtype=torch.int32, device=dev)
@@ -144,7 +145,7 @@ def test_score_select_fused_matches_split(dev, kind, ns):
     """The fused scoring + selection equals t2t_score + t2t_select_run_packed
     bit for bit, and the selection matches the oracle on those scores."""
     from token2tile_amd import ops
-    rng = np.random.default_rng(hash(("fused", kind, ns)) % (2 ** 32))
+    rng = np.random.default_rng(zlib.crc32(f"fused-{kind}-{ns}".encode()))
     H, N, CQ = 2, 3333, 24                      # N not a multiple of the 128-row block
     QU = rng.normal(0, 1, (H, N, 32)).astype(np.float16)
     ck2 = rng.normal(0, 0.5, (H, 2048, 32)).astype(np.float32)
