@@ -140,6 +140,21 @@ int t2t_score_select_packed(const void* QU, const void* cks, const int32_t* kcou
                             const int32_t* qperm, const int32_t* qcounts,
                             const int32_t* ns_dev, int32_t* unip, int32_t* rowcnt,
                             int H, int N, int CQ, void* ws, size_t ws_bytes, void* stream);
+/* Allocation-free t2t_score_select_packed.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It takes no workspace: its scratch (H * (CQ + 1) int32
+ * query-cluster offsets) is a static device array of
+ * T2T_NOALLOC_SCRATCH_INTS entries per GPU, held until the process ends, and
+ * sizes beyond it return T2T_ERR_UNSUPPORTED.  It calls no allocator.  Calls
+ * that overlap on one GPU share that array and race.  Results are
+ * bit-identical to t2t_score_select_packed. */
+#define T2T_NOALLOC_SCRATCH_INTS 262208   /* 64 heads x (4096 + 1) */
+size_t t2t_score_select_noalloc_max_ints(void);
+int t2t_score_select_packed_noalloc(const void* QU, const void* cks, const int32_t* kcounts,
+                                    const int32_t* qperm, const int32_t* qcounts,
+                                    const int32_t* ns_dev, int32_t* unip, int32_t* rowcnt,
+                                    int H, int N, int CQ, void* stream);
 /* Byte-per-cluster union uni[h, t, c] in {0, 1}, [H, CQ, CK] uint8.
  * Replaces ext.run, select_union/src/main.cpp:5-19 (kernel.cu:414-440). */
 int t2t_select_run(const void* gl, const int32_t* kcounts,

@@ -62,3 +62,16 @@ def test_bad_sizes_rejected():
                          1, 100, 8, 2048, 0, p, 16, None) == 2           # workspace too small
     assert b"workspace" in L.t2t_last_error()
     assert L.t2t_select_run_split_packed(p, p, p, p, 0, p, p, p, 1, 8, 4, p, 1 << 20, None) == 1
+
+
+def test_noalloc_select_rejects_oversized_scratch():
+    """The allocation-free fused selection refuses shapes whose offsets do not
+    fit its static scratch, before touching the GPU."""
+    from token2tile_amd import _lib
+    L = _lib.lib()
+    p = ctypes.c_void_p(16)
+    cap = L.t2t_score_select_noalloc_max_ints()
+    assert cap == 64 * 4097
+    assert L.t2t_score_select_packed_noalloc(p, p, p, p, p, p, p, p, 65, 8192, 4096, None) == 4
+    assert b"static scratch" in L.t2t_last_error()
+    assert L.t2t_score_select_packed_noalloc(None, p, p, p, p, p, p, p, 1, 8192, 16, None) == 1

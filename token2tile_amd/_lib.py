@@ -36,6 +36,9 @@ SIGNATURES = {
     "t2t_select_ws_bytes": (c_size_t, [c_int, c_int, c_int]),
     "t2t_score_select_packed": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, _P,
                                         c_size_t, _P]),
+    "t2t_score_select_noalloc_max_ints": (c_size_t, []),
+    "t2t_score_select_packed_noalloc": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int,
+                                                c_int, _P]),
     "t2t_select_run_packed": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int, c_int, c_int, _P,
                                       c_size_t, _P]),
     "t2t_select_run_split_packed": (c_int, [_P, _P, _P, _P, c_int, _P, _P, _P, c_int, c_int,

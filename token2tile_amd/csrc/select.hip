@@ -15,6 +15,7 @@
 // the run crosses into the next cluster, so the union needs no partial
 // buffers.
 #include "t2t_common.h"
+#include <mutex>
 
 #define SEL_NC 2048
 #define SEL_WAVES 4
@@ -487,6 +488,19 @@ static int select_common(const void* gl, const int32_t* kcounts, const int32_t* 
   return T2T_OK;
 }
 
+static int score_select_launch(const void* QU, const void* cks, const int32_t* kcounts,
+                               const int32_t* qperm, const int32_t* qcounts,
+                               const int32_t* ns_dev, int32_t* unip, int32_t* rowcnt, int H,
+                               int N, int CQ, int32_t* off, hipStream_t st) {
+  hipLaunchKernelGGL(select_prep_kernel, dim3(H), dim3(1024), 0, st, qcounts, off, unip, CQ);
+  T2T_LAUNCH_CHECK("score_select prep");
+  hipLaunchKernelGGL(score_select_kernel, dim3(cdiv(N, SF_ROWS * SF_BATCHES), H),
+                     dim3(SF_WAVES * 64), 0, st, (const uint16_t*)QU, (const uint16_t*)cks,
+                     kcounts, qperm, off, ns_dev, unip, rowcnt, N, CQ);
+  T2T_LAUNCH_CHECK("score_select");
+  return T2T_OK;
+}
+
 extern "C" int t2t_score_select_packed(const void* QU, const void* cks, const int32_t* kcounts,
                                        const int32_t* qperm, const int32_t* qcounts,
                                        const int32_t* ns_dev, int32_t* unip, int32_t* rowcnt,
@@ -501,16 +515,73 @@ extern "C" int t2t_score_select_packed(const void* QU, const void* cks, const in
                   t2t_select_ws_bytes(H, N, CQ));
     return T2T_ERR_WORKSPACE;
   }
-  hipStream_t st = (hipStream_t)stream;
   WsCarver w(ws);
   int32_t* off = w.take<int32_t>((size_t)H * (CQ + 1));
-  hipLaunchKernelGGL(select_prep_kernel, dim3(H), dim3(1024), 0, st, qcounts, off, unip, CQ);
-  T2T_LAUNCH_CHECK("score_select prep");
-  hipLaunchKernelGGL(score_select_kernel, dim3(cdiv(N, SF_ROWS * SF_BATCHES), H),
-                     dim3(SF_WAVES * 64), 0, st, (const uint16_t*)QU, (const uint16_t*)cks,
-                     kcounts, qperm, off, ns_dev, unip, rowcnt, N, CQ);
-  T2T_LAUNCH_CHECK("score_select");
+  return score_select_launch(QU, cks, kcounts, qperm, qcounts, ns_dev, unip, rowcnt, H, N, CQ, off,
+                             (hipStream_t)stream);
+}
+
+// ---- the allocation-free variant -------------------------------------------
+// Its only scratch (the query-cluster offsets, H * (CQ + 1) int32) lives in a
+// file-scope device array.  Every GPU holds its own copy of the array at its
+// own address; the host keeps that address per device, taken once with
+// hipGetSymbolAddress while the device is current (the array's name is not a
+// device address in host code).  select_prep_kernel writes every offset of
+// the call before the selection reads it, so nothing needs clearing.  Calls
+// that overlap on one GPU share the array and race.
+static __device__ __align__(256) int32_t scratch[T2T_NOALLOC_SCRATCH_INTS];
+
+#define T2T_MAX_DEVICES 64
+static std::mutex g_scratch_mu;
+static int32_t* g_scratch_ptr[T2T_MAX_DEVICES];
+
+static int noalloc_scratch(int32_t** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    t2t_set_error("score_select_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return T2T_ERR_LAUNCH;
+  }
+  if (dev < 0 || dev >= T2T_MAX_DEVICES) {
+    t2t_set_error("score_select_noalloc: device %d outside [0, %d)", dev, T2T_MAX_DEVICES);
+    return T2T_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      t2t_set_error("score_select_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return T2T_ERR_LAUNCH;
+    }
+    g_scratch_ptr[dev] = (int32_t*)p;
+  }
+  *out = g_scratch_ptr[dev];
   return T2T_OK;
+}
+
+extern "C" size_t t2t_score_select_noalloc_max_ints(void) { return T2T_NOALLOC_SCRATCH_INTS; }
+
+extern "C" int t2t_score_select_packed_noalloc(const void* QU, const void* cks,
+                                               const int32_t* kcounts, const int32_t* qperm,
+                                               const int32_t* qcounts, const int32_t* ns_dev,
+                                               int32_t* unip, int32_t* rowcnt, int H, int N,
+                                               int CQ, void* stream) {
+  T2T_REQUIRE(QU && cks && kcounts && qperm && qcounts && ns_dev && unip && rowcnt,
+              "score_select_noalloc: null pointer");
+  T2T_REQUIRE(H > 0 && N > 0 && CQ > 0, "score_select_noalloc: H=%d N=%d CQ=%d", H, N, CQ);
+  T2T_REQUIRE(N < 524288, "score_select_noalloc: N=%d must be < 524288", N);
+  if ((size_t)H * (size_t)(CQ + 1) > (size_t)T2T_NOALLOC_SCRATCH_INTS) {
+    t2t_set_error("score_select_noalloc: H * (CQ + 1) = %zu offsets exceed the %d-entry "
+                  "static scratch (use t2t_score_select_packed with a workspace)",
+                  (size_t)H * (size_t)(CQ + 1), T2T_NOALLOC_SCRATCH_INTS);
+    return T2T_ERR_UNSUPPORTED;
+  }
+  int32_t* off = nullptr;
+  int rc = noalloc_scratch(&off);
+  if (rc) return rc;
+  return score_select_launch(QU, cks, kcounts, qperm, qcounts, ns_dev, unip, rowcnt, H, N, CQ, off,
+                             (hipStream_t)stream);
 }
 
 extern "C" int t2t_select_run_packed(const void* gl, const int32_t* kcounts, const int32_t* qperm,
