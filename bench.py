@@ -11,8 +11,10 @@ between), so ms/step is the R=4-weighted mean.  Full and reuse calls are
 also timed separately, per stage, with HIP events on the operator's stream.
 
 Also measured: dense bf16 attention on the same GPU (this library's tile
-kernel with an all-ones union, and torch SDPA), the roofline fraction of
-the tile-attention kernel, and the CPU oracle on the CPU plumbing config.
+kernel with an all-ones union, and torch SDPA), the time of a dense call
+at the bf16 MFMA peak, init_state cold (first call of the process) and
+warm, the roofline fraction of the tile-attention kernel, and the CPU
+oracle on the CPU plumbing config on one host thread.
 
 Prints one JSON line.  Usage: python bench.py [--steps K] [--warmup W]
 """
@@ -35,13 +37,13 @@ HBM_PEAK_GBS = 8000.0
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=12)
-    p.add_argument("--warmup", type=int, default=4)
+    p.add_argument("--steps", type=int, default=52)
+    p.add_argument("--warmup", type=int, default=8)
     p.add_argument("--config", default="wan720p")
     p.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-dense", action="store_true")
-    p.add_argument("--sdpa", action="store_true", help="also time torch SDPA (slow at 720p)")
+    p.add_argument("--no-sdpa", action="store_true", help="skip the torch SDPA dense baseline")
     p.add_argument("--calibrate", action="store_true",
                    help="run one row-permuting copy of K (gather_rows_kernel, known bytes) before "
                         "the warm-up, as the scale reference of FETCH_SIZE/WRITE_SIZE counter runs")
@@ -65,8 +67,10 @@ def traffic_bytes(config, dtype):
 
 def cpu_baseline():
     """The CPU oracle (numpy restatement of the reference semantics) timed
-    on one full call of the CPU plumbing config."""
+    on one full call of the CPU plumbing config, on one host thread (the
+    BLAS pool is limited to one thread; the rest is single-threaded numpy)."""
     import numpy as np
+    from threadpoolctl import threadpool_limits
     from oracle import t2t_oracle as O
     from token2tile_amd.synth import CONFIGS, budget, generate_np
     H, N, grid, frac, CQ = CONFIGS["cpu_plumbing"]
@@ -77,13 +81,16 @@ def cpu_baseline():
     rng = np.random.default_rng(0)
     st = dict(Uq=Uq, Uk=Uk, ck=KU[:, np.sort(rng.choice(N, 2048, replace=False))],
               cq=QU[:, np.sort(rng.choice(N, CQ, replace=False))])
-    t0 = time.perf_counter()
-    O.full_call(q, k, v, st, budget(N, frac), CQ)
-    dt = time.perf_counter() - t0
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(dt * 1e3, 1), "unit": "ms/call", "cores": threads, "kind": "port",
-            "sample": f"one structure-rebuilding call of the numpy oracle on the CPU plumbing "
-                      f"config (H={H}, N={N}, CQ={CQ}, ns={budget(N, frac)}, fp32/fp64)"}
+    calls = 2
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            O.full_call(q, k, v, st, budget(N, frac), CQ)
+        dt = (time.perf_counter() - t0) / calls
+    return {"value": round(dt * 1e3, 1), "unit": "ms/call", "cores": 1, "kind": "port",
+            "sample": f"mean of {calls} structure-rebuilding calls of the numpy oracle on the CPU "
+                      f"plumbing config (H={H}, N={N}, CQ={CQ}, ns={budget(N, frac)}, fp32/fp64), "
+                      f"one host thread"}
 
 
 def main():
@@ -105,11 +112,19 @@ def main():
     q, k, v = generate(H, N, grid=grid, seed=0, device=dev, dtype=dt)
     deploy = MaskedStepDeploy(H, N, CQ, s_frac=frac, mask_refresh=4, device=dev)
     torch.cuda.synchronize()
+    # init_state, cold: the first call of the process, which also pays the
+    # one-time set-up of the eigensolver and BLAS libraries; warm: a second
+    # request on fresh inputs (what every later request and layer pays)
+    t0 = time.perf_counter()
+    deploy.init_state(*generate(H, N, grid=grid, seed=1, device=dev, dtype=dt)[:2], seed=1)
+    torch.cuda.synchronize()
+    init_cold_ms = (time.perf_counter() - t0) * 1e3
     t0 = time.perf_counter()
     state = deploy.init_state(q, k, seed=0)
     torch.cuda.synchronize()
     init_ms = (time.perf_counter() - t0) * 1e3
-    print(f"[bench] init_state {init_ms:.1f} ms", file=sys.stderr, flush=True)
+    print(f"[bench] init_state cold {init_cold_ms:.1f} ms, warm {init_ms:.1f} ms", file=sys.stderr,
+          flush=True)
     if args.calibrate:
         # reads H*N*256 B of k plus the H*N int32 permutation, writes H*N*256 B
         perm = torch.argsort(torch.rand(H, N, device=dev), dim=1).to(torch.int32)
@@ -202,17 +217,24 @@ def main():
         dense_ms = a.elapsed_time(b) / reps
         result_dense["dense_tile_kernel_ms"] = round(dense_ms, 3)
         result_dense["dense_tile_kernel_tflops"] = round(dense_flops / (dense_ms * 1e-3) / 1e12, 1)
-        if args.sdpa:
+        if not args.no_sdpa:
             qq, kk, vv = (x.unsqueeze(0) for x in (q, k, v))
             torch.nn.functional.scaled_dot_product_attention(qq, kk, vv)
             torch.cuda.synchronize()
             a.record()
-            torch.nn.functional.scaled_dot_product_attention(qq, kk, vv)
+            for _ in range(reps):
+                torch.nn.functional.scaled_dot_product_attention(qq, kk, vv)
             b.record()
             torch.cuda.synchronize()
-            result_dense["dense_sdpa_ms"] = round(a.elapsed_time(b), 3)
+            result_dense["dense_sdpa_ms"] = round(a.elapsed_time(b) / reps, 3)
+            result_dense["speedup_vs_sdpa"] = round(result_dense["dense_sdpa_ms"] / value, 3)
+            del qq, kk, vv
         best_dense = min(v_ for k_, v_ in result_dense.items() if k_.endswith("_ms"))
         result_dense["speedup_vs_dense"] = round(best_dense / value, 3)
+    # a dense call at the bf16 MFMA peak: the bound no dense kernel can beat
+    dense_peak_ms = dense_flops / (MFMA_BF16_PEAK_TFLOPS * 1e12) * 1e3
+    result_dense["dense_at_peak_ms"] = round(dense_peak_ms, 3)
+    result_dense["speedup_vs_dense_at_peak"] = round(dense_peak_ms / value, 3)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -238,7 +260,7 @@ def main():
         "full_call_ms": round(full_ms, 3),
         "reuse_call_ms": round(reuse_ms, 3),
         "stage_ms": stage_ms,
-        "init_state_ms": round(init_ms, 1),
+        "init_state_ms": {"cold": round(init_cold_ms, 1), "warm": round(init_ms, 1)},
         "effective_tflops": round(dense_flops / (value * 1e-3) / 1e12, 1),
         "executed_tflops": round((attn_flops + tail_flops) / (value * 1e-3) / 1e12, 1),
         "mean_kv_len": round(rows_kv / (H * N), 1),
