@@ -27,3 +27,20 @@ def dev():
         pytest.skip("no GPU in this environment")
     import torch
     return torch.device("cuda", 0)
+
+
+# figures a GPU test measures (step times, ratios), printed in the run's
+# terminal summary so that they survive a quiet (-q) run's output
+_METRICS: dict = {}
+
+
+@pytest.fixture
+def metrics():
+    return _METRICS
+
+
+def pytest_terminal_summary(terminalreporter):
+    if _METRICS:
+        terminalreporter.write_sep("-", "t2t measured figures")
+        for k in sorted(_METRICS):
+            terminalreporter.write_line(f"{k} = {_METRICS[k]}")
