@@ -302,6 +302,18 @@ int t2t_det_centroid_update(const void* x, const int32_t* labels, const void* ol
                             void* out, int32_t* counts,
                             int H, int N, int C, int D,
                             void* ws, size_t ws_bytes, void* stream);
+/* Centroid update with value statistics: labels are grouped by a stable
+ * counting sort; per cluster c with n rows, cent[h, c] = fp32 sum of x rows /
+ * n (empty: fp32(old[h, c])) and, when v is given, vmean[h, c] = fp32 sum of
+ * v rows / max(n, 1); counts[h, c] = n.  The sums run in row order (the
+ * reference adds with fp32 atomics in no fixed order), so results agree with
+ * it to fp32 rounding and are the same on every call.  x [H, N, D] fp16,
+ * D == 32; v [H, N, 128] (v_dtype) or NULL; ws >= t2t_det_update_ws_bytes.
+ * Replaces fused_update_vstats, operator/fused_update_vstats.py:72-115. */
+int t2t_fused_update_vstats(const void* x, const int32_t* labels, const void* old,
+                            const void* v, int v_dtype, float* cent, int32_t* counts,
+                            float* vmean, int H, int N, int C, int D, void* ws,
+                            size_t ws_bytes, void* stream);
 /* G[h] = x[h]^T x[h] / N in fp64 ([H, D, D]); bf16 x is rounded to fp16
  * first.  Replaces the Gram products of online_u,
  * operator/deploy_step.py:135-137. D <= 128.  ws holds the per-split partial

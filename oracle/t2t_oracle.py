@@ -520,6 +520,36 @@ def det_centroid_update(x, labels, old):
     return out, counts
 
 
+def fused_update_vstats(x, labels, old, v=None):
+    """fp32 centroid means and per-cluster value means.
+
+    fused_update_vstats.py:72-115: per cluster, fp32 sums of the x rows (and
+    v rows); new centroid = sum / n, an empty cluster keeps fp32(old); value
+    mean = sum / max(n, 1).  The reference adds with fp32 atomics in no fixed
+    order; this restatement adds in row order (the order of the stable
+    cluster grouping), which is the order the HIP kernel uses.  Pinned in
+    tests/test_oracle_kmeans.py against exact (math.fsum) means to the fp32
+    rounding bound, and the empty-cluster rules.
+    Returns (cent fp32 [H, C, D], counts int32 [H, C], vmean fp32 or None).
+    """
+    x = np.asarray(x, dtype=np.float16)
+    H, N, D = x.shape
+    C = old.shape[1]
+    perm, counts = stable_perm(np.asarray(labels, dtype=np.int32), C)
+    cent = np.empty((H, C, D), dtype=np.float32)
+    vmean = None if v is None else np.empty((H, C, v.shape[2]), dtype=np.float32)
+    for h in range(H):
+        n = counts[h].astype(np.float32)[:, None]
+        sk = _segment_sums_sequential(x[h], perm[h], counts[h])
+        with np.errstate(invalid="ignore", divide="ignore"):
+            mean = (sk / n).astype(np.float32)
+        cent[h] = np.where(counts[h][:, None] > 0, mean, old[h].astype(np.float32))
+        if v is not None:
+            sv = _segment_sums_sequential(np.asarray(v[h], dtype=np.float32), perm[h], counts[h])
+            vmean[h] = (sv / np.maximum(n, np.float32(1.0))).astype(np.float32)
+    return cent, counts, vmean
+
+
 # ---------------------------------------------------------------------------
 # whole call
 # ---------------------------------------------------------------------------

@@ -507,3 +507,36 @@ def test_gram_full_width(dev, dtype, N, D):
     ref = np.einsum("hni,hnj->hij", xd, xd) / N
     assert np.allclose(G, ref, rtol=1e-12, atol=1e-12)
     assert np.array_equal(G, c(ops.gram(xt)))              # same result on every call
+
+
+@pytest.mark.parametrize("vdtype", [None, torch.float16, torch.bfloat16])
+def test_fused_update_vstats_matches_oracle(dev, vdtype):
+    """The reference's fused_update_vstats surface: fp32 centroid and value
+    means bit-exact with the oracle (both sum in row order), fp16 / v-dtype
+    outputs unless return_fp32, out-of-range labels rejected."""
+    from token2tile_amd import deploy_step
+    rng = np.random.default_rng(22)
+    H, N, C = 2, 3000, 100
+    x = rng.normal(0, 1, (H, N, 32)).astype(np.float16)
+    labels = rng.integers(0, C - 5, (H, N)).astype(np.int32)
+    old = rng.normal(0, 1, (H, C, 32)).astype(np.float16)
+    tv = None if vdtype is None else g(rng.normal(0, 2, (H, N, 128)).astype(np.float32), dev).to(vdtype)
+    vf = None if tv is None else c(tv.float())
+    ecent, ecounts, evmean = O.fused_update_vstats(x, labels, old, vf)
+    cent, counts, vmean = deploy_step.fused_update_vstats(g(x, dev), g(labels, dev), g(old, dev),
+                                                          tv, return_fp32=True)
+    assert cent.dtype == torch.float32 and np.array_equal(c(cent), ecent)
+    assert np.array_equal(c(counts), ecounts)
+    if tv is None:
+        assert vmean is None
+    else:
+        assert vmean.dtype == torch.float32 and np.array_equal(c(vmean), evmean)
+    cent16, _, vmean16 = deploy_step.fused_update_vstats(g(x, dev), g(labels, dev).long(),
+                                                         g(old, dev), tv)
+    assert cent16.dtype == torch.float16 and torch.equal(cent16, cent.to(torch.float16))
+    if tv is not None:
+        assert vmean16.dtype == vdtype and torch.equal(vmean16, vmean.to(vdtype))
+    bad = g(labels, dev).clone()
+    bad[0, 0] = C
+    with pytest.raises(ValueError, match="labels"):
+        deploy_step.fused_update_vstats(g(x, dev), bad, g(old, dev))

@@ -109,3 +109,36 @@ def test_det_centroid_update_matches_exact_mean():
         exact = x[0, rows].astype(np.float64).mean(0)
         assert np.allclose(new[0, c].astype(np.float64), exact, rtol=1e-3, atol=1e-3)
     assert np.all(new[0, 10:] == 0) and counts[0, 10:].sum() == 0
+
+
+def test_fused_update_vstats_fp32_means():
+    """The fp32 mean update (fused_update_vstats.py:72-115): centroid and
+    value means within the fp32 rounding bound of the exact (fsum) means,
+    empty clusters keep the old centroid and get a zero value mean, counts
+    are the bincount."""
+    import math
+    rng = np.random.default_rng(21)
+    H, N, C = 2, 700, 40
+    x = rng.normal(0, 2, (H, N, 32)).astype(np.float16)
+    v = rng.normal(0, 3, (H, N, 128)).astype(np.float16).astype(np.float32)
+    labels = rng.integers(0, C - 3, (H, N)).astype(np.int32)     # clusters C-3.. stay empty
+    old = rng.normal(0, 1, (H, C, 32)).astype(np.float16)
+    cent, counts, vmean = O.fused_update_vstats(x, labels, old, v)
+    eps = 2.0 ** -24
+    for h in range(H):
+        assert np.array_equal(counts[h], np.bincount(labels[h], minlength=C))
+        for c in range(C):
+            rows = np.flatnonzero(labels[h] == c)
+            n = rows.size
+            if n == 0:
+                assert np.array_equal(cent[h, c], old[h, c].astype(np.float32))
+                assert not vmean[h, c].any()
+                continue
+            for arr, got in ((x[h].astype(np.float64), cent[h, c]), (v[h].astype(np.float64),
+                                                                      vmean[h, c])):
+                exact = np.array([math.fsum(arr[rows, d]) for d in range(arr.shape[1])]) / n
+                bound = (n + 2) * eps * np.abs(arr[rows]).sum(0) / n + 1e-30
+                assert np.all(np.abs(got - exact) <= bound)
+    # without v: the same centroids, no value means
+    cent2, counts2, none = O.fused_update_vstats(x, labels, old)
+    assert none is None and np.array_equal(cent2, cent) and np.array_equal(counts2, counts)

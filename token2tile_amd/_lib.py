@@ -81,6 +81,8 @@ SIGNATURES = {
     "t2t_det_update_ws_bytes": (c_size_t, [c_int, c_int, c_int]),
     "t2t_det_centroid_update": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, _P,
                                         c_size_t, _P]),
+    "t2t_fused_update_vstats": (c_int, [_P, _P, _P, _P, c_int, _P, _P, _P, c_int, c_int, c_int,
+                                        c_int, _P, c_size_t, _P]),
     "t2t_gram_ws_bytes": (c_size_t, [c_int, c_int, c_int]),
     "t2t_gram": (c_int, [_P, c_int, _P, c_int, c_int, c_int, _P, c_size_t, _P]),
 }

@@ -795,6 +795,84 @@ extern "C" size_t t2t_det_update_ws_bytes(int H, int N, int C) {
   return det_layout(H, N, C, nullptr).total;
 }
 
+// ---------------------------------------------------------------------------
+// fp32 centroid means and per-cluster value means (the reference's
+// fused_update_vstats): one wave per cluster sums its rows in sorted order,
+// fp32 and sequential per dim (lanes 0..31: one dim of x each; all lanes: two
+// dims of v each).  Empty clusters: centroid = fp32(old), value mean = 0.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void seg_mean_kernel(
+    const uint16_t* __restrict__ X, const uint16_t* __restrict__ V,
+    const int32_t* __restrict__ perm, const int32_t* __restrict__ counts,
+    const int32_t* __restrict__ cbase, const uint16_t* __restrict__ old,
+    float* __restrict__ cent, float* __restrict__ vmean, int N, int C) {
+  const int h = blockIdx.y;
+  const int l = threadIdx.x & 63;
+  const int c = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (c >= C) return;
+  const int n = counts[(size_t)h * C + c];
+  const int32_t* ph = perm + (size_t)h * N + cbase[(size_t)h * C + c];
+  const uint16_t* xh = X + (size_t)h * N * KM_R;
+  const uint32_t* vh = V ? (const uint32_t*)(V + (size_t)h * N * 128) : nullptr;
+  float ax = 0.f, v0 = 0.f, v1 = 0.f;
+  for (int i0 = 0; i0 < n; i0 += 64) {
+    const int myrow = i0 + l < n ? ph[i0 + l] : 0;
+    const int m = n - i0 < 64 ? n - i0 : 64;
+    for (int i = 0; i < m; ++i) {
+      const int rw = __builtin_amdgcn_readlane(myrow, i);
+      if (l < KM_R) ax += h2f(xh[(size_t)rw * KM_R + l]);
+      if (vh) {
+        const uint32_t u = vh[(size_t)rw * 64 + l];
+        v0 += T::to_f((uint16_t)(u & 0xffff));
+        v1 += T::to_f((uint16_t)(u >> 16));
+      }
+    }
+  }
+  if (l < KM_R) {
+    const size_t o = ((size_t)h * C + c) * KM_R + l;
+    cent[o] = n ? ax / (float)n : h2f(old[o]);
+  }
+  if (vh) {
+    const float d = n ? (float)n : 1.0f;
+    float* vo = vmean + ((size_t)h * C + c) * 128 + 2 * l;
+    vo[0] = v0 / d;
+    vo[1] = v1 / d;
+  }
+}
+
+extern "C" int t2t_fused_update_vstats(const void* x, const int32_t* labels, const void* old,
+                                       const void* v, int v_dtype, float* cent, int32_t* counts,
+                                       float* vmean, int H, int N, int C, int D, void* ws,
+                                       size_t ws_bytes, void* stream) {
+  T2T_REQUIRE(x && labels && old && cent && counts, "fused_update_vstats: null pointer");
+  T2T_REQUIRE(!v || vmean, "fused_update_vstats: v given without vmean");
+  T2T_REQUIRE(!v || v_dtype == T2T_F16 || v_dtype == T2T_BF16, "fused_update_vstats: dtype %d",
+              v_dtype);
+  T2T_REQUIRE(H > 0 && N > 0 && C >= 1 && C <= KM_MAXC, "fused_update_vstats: H=%d N=%d C=%d", H,
+              N, C);
+  T2T_REQUIRE(D == KM_R, "fused_update_vstats: D=%d (built for %d)", D, KM_R);
+  const size_t need = det_layout(H, N, C, nullptr).total;
+  if (!ws || ws_bytes < need) {
+    t2t_set_error("fused_update_vstats: workspace %zu < %zu bytes", ws_bytes, need);
+    return T2T_ERR_WORKSPACE;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  DetWs w = det_layout(H, N, C, ws);
+  KM_CHECK(run_sort(labels, counts, w.cbase, w.perm, w.chist, H, N, C, st));
+  const dim3 g(cdiv(C, 4), H);
+  if (v && v_dtype == T2T_BF16)
+    hipLaunchKernelGGL(seg_mean_kernel<BF16T>, g, dim3(256), 0, st, (const uint16_t*)x,
+                       (const uint16_t*)v, w.perm, counts, w.cbase, (const uint16_t*)old, cent,
+                       vmean, N, C);
+  else
+    hipLaunchKernelGGL(seg_mean_kernel<F16T>, g, dim3(256), 0, st, (const uint16_t*)x,
+                       (const uint16_t*)v, w.perm, counts, w.cbase, (const uint16_t*)old, cent,
+                       vmean, N, C);
+  T2T_LAUNCH_CHECK("fused_update_vstats");
+  return T2T_OK;
+}
+
 extern "C" int t2t_det_centroid_update(const void* x, const int32_t* labels, const void* old,
                                        void* out, int32_t* counts, int H, int N, int C, int D,
                                        void* ws, size_t ws_bytes, void* stream) {

@@ -99,16 +99,23 @@ def fast_assign(x, centroids, out=None, **_tuning):
     return ops.fast_assign_labels(x.contiguous(), centroids.contiguous(), out=out)
 
 
-def fused_update_vstats(ku, labels, old_centroids, v=None, **_kw):
-    """Centroid update with empty clusters keeping the old centroid; returns
-    (new_centroids fp16, counts int32, None) like fused_update_vstats.py:72-115
-    (value statistics are not produced).  The sums are the deterministic
-    int64 fixed-point ones of the reference backend (t2t_attn.py:242-257)."""
-    if v is not None:
-        raise NotImplementedError("t2t: value statistics come from t2t_kmm_run")
-    new, counts = ops.det_centroid_update(ku.contiguous(), labels.to(torch.int32).contiguous(),
-                                          old_centroids.contiguous())
-    return new, counts, None
+def fused_update_vstats(ku, labels, old_centroids, v=None, *, BLOCK_N=32, num_warps=2,
+                        return_fp32=False):
+    """One pass producing new centroids [H, C, DK], counts [H, C] int32 and,
+    when ``v`` is given, the per-cluster mean values [H, C, DV]
+    (fused_update_vstats.py:72-115).  Sums are fp32; an empty cluster keeps
+    its old centroid and has a zero mean value.  Outputs are cast to the
+    dtype of ku / v unless ``return_fp32``.  ``BLOCK_N`` and ``num_warps``
+    are the reference's Triton tuning knobs: accepted and ignored."""
+    del BLOCK_N, num_warps
+    cent, counts, vmean = ops.fused_update_vstats(
+        ku.contiguous(), labels.to(torch.int32).contiguous(), old_centroids.contiguous(),
+        None if v is None else v.contiguous())
+    if not return_fp32:
+        cent = cent.to(ku.dtype)
+        if vmean is not None:
+            vmean = vmean.to(v.dtype)
+    return cent, counts, vmean
 
 
 # ---------------------------------------------------------------------------
@@ -247,7 +254,10 @@ class MaskedStepDeploy:
         kept for the whole request; the centroids warm-start every rebuild.
         Initial centroids are KU / QU rows picked by a seeded CPU randperm
         (the same indices as the reference), then ``warm_iters`` Lloyd
-        iterations (nearest centroid + deterministic centroid update)."""
+        iterations: nearest centroid (fast_assign) and the fp32 mean update
+        of fused_update_vstats, as the reference operator's init_state does
+        (deploy_step.py:245-266).  The backend's ``t2t_fast_init`` path keeps
+        the deterministic fixed-point update instead (t2t_attn.py:242-281)."""
         N, r = self.N, self.r
         Uq, Uk = online_u(q, k, r)
         Uq = Uq.to(torch.float16).contiguous()
@@ -260,10 +270,10 @@ class MaskedStepDeploy:
         ck = KU[:, kidx, :].contiguous()
         cq = QU[:, qidx, :].contiguous()
         for _ in range(warm_iters):
-            lab = fast_assign(KU, ck)
-            ck, _ = ops.det_centroid_update(KU, lab, ck)
-            lab = fast_assign(QU, cq)
-            cq, _ = ops.det_centroid_update(QU, lab, cq)
+            cent, _, _ = ops.fused_update_vstats(KU, fast_assign(KU, ck), ck, check_labels=False)
+            ck = cent.to(torch.float16)
+            cent, _, _ = ops.fused_update_vstats(QU, fast_assign(QU, cq), cq, check_labels=False)
+            cq = cent.to(torch.float16)
         torch.cuda.synchronize(self.dev)
         return {"Uq": Uq, "Uk": Uk, "ck": ck.contiguous(), "cq": cq.contiguous()}
 

@@ -527,6 +527,33 @@ def det_centroid_update(x, labels, old, stream=None):
     return new, counts
 
 
+def fused_update_vstats(x, labels, old, v=None, stream=None, check_labels=True):
+    """fp32 centroid means (empty clusters keep ``old``), counts, and the
+    fp32 per-cluster means of v when given -> (cent fp32 [H, C, D], counts
+    int32 [H, C], vmean fp32 [H, C, 128] or None).  ``check_labels`` reads
+    the label range back to the host (a synchronisation); callers whose
+    labels come from an assignment kernel pass False."""
+    H, N, D = x.shape
+    C = old.shape[1]
+    dev = _dev(x)
+    _check(x, (H, N, D), _f16, "x", dev)
+    _check(labels, (H, N), _i32, "labels", dev)
+    _check(old, (H, C, D), _f16, "old", dev)
+    if v is not None:
+        _check(v, (H, N, HEAD_DIM), _HALF, "v", dev)
+    if check_labels:
+        lo, hi = (int(t) for t in torch.aminmax(labels))
+        if lo < 0 or hi >= C:
+            raise ValueError(f"t2t: labels must lie in [0, {C}), got [{lo}, {hi}]")
+    cent = torch.empty(H, C, D, dtype=_f32, device=dev)
+    counts = torch.empty(H, C, dtype=_i32, device=dev)
+    vmean = None if v is None else torch.empty(H, C, HEAD_DIM, dtype=_f32, device=dev)
+    ws = _ws(size_query("t2t_det_update_ws_bytes", H, N, C), dev)
+    call("t2t_fused_update_vstats", x, labels, old, v, dtype_code(v.dtype) if v is not None else 0,
+         cent, counts, vmean, H, N, C, D, ws, ws.numel(), stream_handle(stream))
+    return cent, counts, vmean
+
+
 def gram(x, stream=None):
     """x^T x / N per head in fp64: [H, D, D]."""
     H, N, D = x.shape
