@@ -1,7 +1,10 @@
 // S4: per-query key-cluster selection and query-cluster union (gfx950).
 //
 // One wave owns a run of consecutive SORTED query rows (qperm order), so the
-// work is balanced whatever the query-cluster sizes are.  For each row the
+// work is balanced whatever the query-cluster sizes are.  (The fused scoring
+// + selection kernel below first tries a one-pass window around the previous
+// row's crossing key, which resolves nearly every row; the radix passes
+// described here are its fallback and the unfused kernel's method.)  For each row the
 // 2048 fp16 scores sit in registers (lane l holds clusters 512 g + 8 l + j,
 // g < 4, j < 8), and the budget threshold is found exactly with two 8-bit
 // radix passes over a wave-private, size-weighted LDS histogram:
@@ -117,10 +120,13 @@ __device__ inline int find_cross(const int* hist, int base, int ns, int* above, 
 // the clusters with keys >= lo hold >= ns keys: the crossing key is then >= lo
 // and every key at or above it is counted.  Otherwise the row is redone
 // without the bound.
+__device__ inline uint32_t select_bits(const int (&key)[32], const int (&sz)[32], int ns, int vstar,
+                                       int wgt, int weq, int ntie, int* rowcnt);
 #define SEL_NO_BOUND (-65536)
 #define SEL_BOUND_MARGIN 1024  // one binade of fp16 keys
-__device__ inline uint32_t select_row(const int (&key)[32], const int (&sz)[32], int* hist, int ns,
-                                      int lo, int* rowcnt, int* vstar_out) {
+__device__ inline void radix_cross(const int (&key)[32], const int (&sz)[32], int* hist, int ns,
+                                   int lo, int* vstar_out, int* wgt_out, int* weq_out,
+                                   int* ntie_out) {
   const int l = __lane_id();
   // ---- pass 1: high byte ----
   int hb, above1, inbin1, tot1;
@@ -150,10 +156,25 @@ __device__ inline uint32_t select_row(const int (&key)[32], const int (&sz)[32],
   int wgt, weq, tot2, ntie;
   const int lb = find_cross<true>(hist, above1, ns, &wgt, &weq, &tot2, &ntie);
   wave_sync();
-  const int vstar = hsel * 256 + lb;
-  *vstar_out = vstar;
-  // ---- ties at the threshold (ntie clusters hold the key vstar), in
-  //      ascending cluster order ----
+  *vstar_out = hsel * 256 + lb;
+  *wgt_out = wgt;
+  *weq_out = weq;
+  *ntie_out = ntie;
+}
+__device__ inline uint32_t select_row(const int (&key)[32], const int (&sz)[32], int* hist, int ns,
+                                      int lo, int* rowcnt, int* vstar_out) {
+  int wgt, weq, ntie;
+  radix_cross(key, sz, hist, ns, lo, vstar_out, &wgt, &weq, &ntie);
+  return select_bits(key, sz, ns, *vstar_out, wgt, weq, ntie, rowcnt);
+}
+
+// The lane's 32 selection bits given the crossing key vstar of the row, the
+// weight wgt of all keys above it, the weight weq and number ntie of the
+// clusters holding vstar; *rowcnt = selected keys.  Ties at the threshold
+// (ntie > 1) are taken in ascending cluster order.
+__device__ inline uint32_t select_bits(const int (&key)[32], const int (&sz)[32], int ns, int vstar,
+                                       int wgt, int weq, int ntie, int* rowcnt) {
+  const int l = __lane_id();
   uint32_t bits = 0;
   if (ntie == 1) {
     // bit i = key[i] >= vstar, shifted in from bit 31 down: compare into VCC,
@@ -212,6 +233,93 @@ __device__ inline uint32_t select_row(const int (&key)[32], const int (&sz)[32],
   }
   *rowcnt = wgt + cum;
   return gt | (tie & upto);
+}
+
+// Single-pass crossing search in a window of 512 consecutive keys [lo, lo +
+// 512) placed around the previous row's crossing key.  Only the lane's keys
+// at or above lo are visited (a few per lane): a key in the window adds
+// (size << 12) | 1 to its own bin of a wave-private LDS histogram, a key above
+// it adds its size to a register sum; keys below lo are not touched.  The
+// bins then hold the exact weight and cluster count of every key value in the
+// window, and the sum the weight above it.  When the crossing lies in the
+// window (weight above < ns <= weight above + window weight) this gives the
+// crossing key, the weight above it and the weight and count of its clusters
+// without the two radix passes (returns 0); otherwise it returns 1 (crossing
+// above the window) or -1 (below it).
+#define SEL_WIN 512
+#define SEL_WHIST SEL_WIN  // window bins (the radix fallback uses the first 320)
+__device__ inline int window_cross(const int (&key)[32], const uint16_t* krow, const int* ssz,
+                                   int* hist, int ns, int lo, int* vstar, int* wgt, int* weq,
+                                   int* ntie) {
+  const int l = __lane_id();
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    *(u32x4*)(hist + 4 * (l + 64 * i)) = u32x4{0u, 0u, 0u, 0u};
+  // the lane's keys at or above the window's base, as a mask: bit i = key[i]
+  // >= lo, shifted in from bit 31 down (compare into VCC, then m + m + carry)
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 31; i >= 0; --i)
+    asm("v_cmp_ge_i32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
+        : "+v"(m)
+        : "v"(key[i]), "v"(lo)
+        : "vcc");
+  wave_sync();
+  int aw = 0;  // the lane's weight above the window
+  while (__ballot(m != 0u) != 0ull) {  // wave-uniform
+    if (m != 0u) {
+      const int i = __builtin_ctz(m);
+      m &= m - 1u;
+      const int c = 512 * (i >> 3) + 8 * l + (i & 7);  // cluster of key slot i
+      const int d = (int)(int16_t)krow[c] - lo;
+      const int sz = ssz[c];
+      if (d >= SEL_WIN)
+        aw += sz;
+      else
+        atomicAdd(&hist[d], (sz << 12) | 1);
+    }
+  }
+  wave_sync();
+  // lane l scans bins 511 - 8 l .. 504 - 8 l (descending keys)
+  int raw[8];
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    raw[i] = hist[SEL_WIN - 1 - 8 * l - i];
+    s += raw[i] >> 12;
+  }
+  const int above = wave_sum(aw);
+  const int inc = wave_incl_scan(s);
+  const int total = above + __builtin_amdgcn_readlane(inc, 63);
+  wave_sync();
+  if (above >= ns) return 1;  // wave-uniform: the crossing is above the window
+  if (total < ns) return -1;  // below it
+  const int ex = inc - s + above;
+  const bool mine = ex < ns && ex + s >= ns;
+  int bin = 0, ab = 0, raw_b = 0;
+  if (mine) {
+    int cum = ex;
+    bool done = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int w = raw[i] >> 12;
+      if (!done && cum + w >= ns) {
+        bin = SEL_WIN - 1 - 8 * l - i;
+        ab = cum;
+        raw_b = raw[i];
+        done = true;
+      }
+      cum += w;
+    }
+  }
+  const unsigned long long bal = __ballot(mine);
+  const int src = (int)__ffsll((long long)bal) - 1;
+  *vstar = lo + __builtin_amdgcn_readlane(bin, src);
+  *wgt = __builtin_amdgcn_readlane(ab, src);
+  raw_b = __builtin_amdgcn_readlane(raw_b, src);
+  *weq = raw_b >> 12;
+  *ntie = raw_b & 0xfff;
+  return 0;
 }
 
 // publish the lanes' masks into the packed union row (LSB-first words);
@@ -311,11 +419,25 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
 // computes the scores of the batch against 256 of the centroids on MFMA, with
 // the instruction, operand split and fp16 rounding of score_kernel (so the
 // scores, and the selection, are bit-identical to the unfused path), and
-// stores the ordered keys in LDS; then every wave selects 4 of the rows.
-// A work-group walks 16 batches (512 rows): the centroid fragments and
-// cluster sizes it loads once are amortised over them, and the next batch's
-// query rows load while the current batch is being selected.
+// stores the ordered keys in LDS; then the waves select the rows, taking
+// them one at a time from a counter.  A row is searched in a 512-key window
+// around the previous row's crossing (window_cross: a few keys per lane, one
+// histogram pass), then in the window above or below it, and by the radix
+// passes only when both miss (a few rows in 10^4 at 720p).  A work-group
+// walks 16 batches (512 rows): the cluster sizes it loads once are amortised
+// over them, and the next batch's query rows load while the current batch is
+// being selected.  The centroid fragments are reloaded (from L2) per batch,
+// which keeps their 64 registers free during the selection.
 // ---------------------------------------------------------------------------
+// the order keys of a pair of fp16 scores (score_key on each half): the sign
+// of each half spread over it (v_pk_ashrrev_i16), then x ^ (sign & 0x7FFF)
+// per half in one three-input bit operation
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t key_pair(uint32_t x) {
+  const uint32_t sm = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2, x) >> (s16x2){15, 15});
+  return x ^ (sm & 0x7FFF7FFFu);
+}
+
 #define SF_WAVES 8
 #define SF_ROWS 32
 #define SF_BATCHES 16
@@ -327,7 +449,12 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
     const int32_t* __restrict__ off, const int32_t* __restrict__ ns_dev,
     int32_t* __restrict__ unip, int32_t* __restrict__ rowcnt, int N, int CQ) {
   __shared__ __attribute__((aligned(16))) uint16_t sKey[SF_ROWS * SF_PITCH];
-  __shared__ int hist_all[SF_WAVES][SEL_HIST];
+  __shared__ __attribute__((aligned(16))) int hist_all[SF_WAVES][SEL_WHIST];
+  // rows of a batch are handed out one at a time (a counter per batch
+  // parity), so a wave with cheap rows takes more of them
+  __shared__ int sNext[2];
+  __shared__ int sSz[SEL_NC];  // the head's key-cluster sizes
+
   const int h = blockIdx.y;
   const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int jl = l & 31, hh = l >> 5;
@@ -354,16 +481,10 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
   ns = ns < 1 ? 1 : ns;
   ns = ns > ktot ? ktot : ns;
   // centroid fragments of the wave's 256 centroids (the A operands of
-  // score_kernel: row 32 cb + jl, dims 8 hh .. and 16 + 8 hh ..)
-  u32x4 ca0[8], ca1[8];
-  {
-    const uint16_t* ch = cks + ((size_t)h * SEL_NC + 256 * wv + jl) * 32 + 8 * hh;
-#pragma unroll
-    for (int cb = 0; cb < 8; ++cb) {
-      ca0[cb] = *(const u32x4*)(ch + cb * 32 * 32);
-      ca1[cb] = *(const u32x4*)(ch + cb * 32 * 32 + 16);
-    }
-  }
+  // score_kernel: row 32 cb + jl, dims 8 hh .. and 16 + 8 hh ..), loaded
+  // (from L2) for each batch's scoring, so that their 64 registers are free
+  // during the selection
+  const uint16_t* ch = cks + ((size_t)h * SEL_NC + 256 * wv + jl) * 32 + 8 * hh;
   const int32_t* qp = qperm + (size_t)h * N;
   const uint16_t* qh = QU + (size_t)h * N * 32;
   int32_t* uh = unip + (size_t)h * CQ * (SEL_NC / 32);
@@ -384,11 +505,19 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
   };
   u32x4 b0, b1;
   load_rows(base, b0, b1);
+  if (threadIdx.x < 2) sNext[threadIdx.x] = 0;
+  for (int c = threadIdx.x; c < SEL_NC; c += SF_WAVES * 64) sSz[c] = kcounts[(size_t)h * SEL_NC + c];
   for (int b = 0; b < SF_BATCHES; ++b) {
     const int j0 = base + SF_ROWS * b;
     if (j0 >= lim) break;
     {  // scores of rows j0 .. j0 + 31 against the wave's centroids -> keys in LDS
       uint16_t* krow = sKey + jl * SF_PITCH + 256 * wv + 4 * hh;
+      u32x4 ca0[8], ca1[8];
+#pragma unroll
+      for (int cb = 0; cb < 8; ++cb) {
+        ca0[cb] = *(const u32x4*)(ch + cb * 32 * 32);
+        ca1[cb] = *(const u32x4*)(ch + cb * 32 * 32 + 16);
+      }
 #pragma unroll
       for (int cb = 0; cb < 8; ++cb) {
         f32x16 sc = zero16();
@@ -398,11 +527,10 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           u32x2 o;
-          o[0] = (uint32_t)f2h(sc[4 * g + 0]) | ((uint32_t)f2h(sc[4 * g + 1]) << 16);
-          o[1] = (uint32_t)f2h(sc[4 * g + 2]) | ((uint32_t)f2h(sc[4 * g + 3]) << 16);
+          o[0] = Pk<F16T>::pack(sc[4 * g + 0], sc[4 * g + 1]);  // fp32 -> fp16, RNE
+          o[1] = Pk<F16T>::pack(sc[4 * g + 2], sc[4 * g + 3]);
 #pragma unroll
-          for (int w = 0; w < 2; ++w)  // ordered keys of both halves
-            o[w] ^= ((o[w] >> 15) & 0x00010001u) * 0x7FFFu;
+          for (int w = 0; w < 2; ++w) o[w] = key_pair(o[w]);  // ordered keys of both halves
           *(u32x2*)(krow + 32 * cb + 8 * g) = o;
         }
       }
@@ -410,11 +538,15 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
     // the next batch's rows load while this batch is selected
     load_rows(j0 + SF_ROWS, b0, b1);
     __syncthreads();
+    // every wave is past the previous batch: its counter can be reset
+    if (threadIdx.x == 0) sNext[(b + 1) & 1] = 0;
 #pragma unroll 1
-    for (int i = 0; i < SF_ROWS / SF_WAVES; ++i) {
-      const int r = (SF_ROWS / SF_WAVES) * wv + i;
+    for (;;) {
+      int r = 0;
+      if (l == 0) r = atomicAdd(&sNext[b & 1], 1);
+      r = __builtin_amdgcn_readfirstlane(r);
       const int j = j0 + r;
-      if (j >= lim) break;  // wave-uniform
+      if (r >= SF_ROWS || j >= lim) break;  // wave-uniform (rows only grow per wave)
       if (j >= tend) {      // wave-uniform: every lane takes part in the shuffles
         if (t >= 0) flush_union(acc, uh + (size_t)t * (SEL_NC / 32));
         acc = 0;
@@ -441,7 +573,22 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
         }
       }
       int rc;
-      acc |= select_row(key, sz, hist, ns, klo, &rc, &vstar);
+      // the window around the previous row's crossing first; the full search
+      // when the crossing lies outside it (or for the wave's first row)
+      int vs, wgt, weq, ntie;
+      int where = 0;
+      if (klo != SEL_NO_BOUND) {
+        const int lo = vstar - SEL_WIN / 2;
+        where = window_cross(key, kr, sSz, hist, ns, lo, &vs, &wgt, &weq, &ntie);
+        if (where > 0)  // the crossing is above the window: the window above it
+          where = window_cross(key, kr, sSz, hist, ns, lo + SEL_WIN, &vs, &wgt, &weq, &ntie);
+        else if (where < 0)  // below it: the window below
+          where = window_cross(key, kr, sSz, hist, ns, lo - SEL_WIN, &vs, &wgt, &weq, &ntie);
+      }
+      if (where != 0 || klo == SEL_NO_BOUND)
+        radix_cross(key, sz, hist, ns, klo, &vs, &wgt, &weq, &ntie);
+      vstar = vs;
+      acc |= select_bits(key, sz, ns, vstar, wgt, weq, ntie, &rc);
       klo = vstar - SEL_BOUND_MARGIN;
       if (l == 0) rowcnt[(size_t)h * N + qp[j]] = rc;
     }
