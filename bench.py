@@ -198,11 +198,11 @@ def main():
         # dense baseline 1: this library's tile kernel over an all-ones union
         ones = torch.full((H, CQ, 64), -1, dtype=torch.int32, device=dev)
         plan = ops.tile_plan(snap["tile_sizes"], snap["counts"], ones, N)
-        io = deploy._buffers(dt)
-        kp = ops.fast_gather(k, snap["kperm"])  # K in cluster order for the dense launch
+        kp = ops.fast_gather(k, snap["kperm"])  # K and V in cluster order for the dense launch
+        vp = ops.fast_gather(v, snap["kperm"])
         ao = torch.empty_like(q)
         lse = torch.empty(H, N, device=dev, dtype=torch.float32)
-        ops.tile_attn_exact(q, kp, io["vp"], snap["counts"], ones, snap["qperm"], plan,
+        ops.tile_attn_exact(q, kp, vp, snap["counts"], ones, snap["qperm"], plan,
                             attn_out=ao, lse=lse)
         torch.cuda.synchronize()
         a = torch.cuda.Event(enable_timing=True)
@@ -210,7 +210,7 @@ def main():
         reps = 2
         a.record()
         for _ in range(reps):
-            ops.tile_attn_exact(q, kp, io["vp"], snap["counts"], ones, snap["qperm"], plan,
+            ops.tile_attn_exact(q, kp, vp, snap["counts"], ones, snap["qperm"], plan,
                                 attn_out=ao, lse=lse)
         b.record()
         torch.cuda.synchronize()

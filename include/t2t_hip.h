@@ -64,7 +64,8 @@ int t2t_project(const void* x, int x_dtype, const void* U, void* out,
 size_t t2t_kmm_ws_bytes(int H, int N, int CQ, int CK);
 /* One warm-started k-means update: query labels over two assignment passes
  * (qlab, cq2, qcounts, qperm), key labels in one pass (klab, kcounts,
- * kperm, ck2 fp32), cluster-ordered V (V_sorted, dtype v_dtype), value sums
+ * kperm, ck2 fp32), cluster-ordered V (V_sorted, dtype v_dtype; NULL: not
+ * written, for callers that read V through kperm), value sums
  * sumv = fp16(vsum / lam) with lam = max(1, max|vsum| / 32768).  Rows
  * >= N - pin_tail get key label CK - 1.  Deterministic.
  * Replaces kmm_ext.run, kernels/kmeans_maintain/src/main.cpp:20-46
@@ -79,7 +80,8 @@ int t2t_kmm_run(const void* QU, const void* KU, const void* V, int v_dtype,
                 void* ws, size_t ws_bytes, void* stream);
 /* Workspace bytes for the two value-statistics calls. */
 size_t t2t_vstats_ws_bytes(int H, int N, int CK);
-/* Reuse call: V_sorted = V[kperm], sumv, lam from this call's V.
+/* Reuse call: V_sorted = V[kperm] (NULL: not written), sumv, lam from this
+ * call's V.
  * Replaces kmm_ext.run_vstats_gather, kmeans_maintain/src/main.cpp:63-78
  * (kernels.cu:900-923). */
 int t2t_kmm_run_vstats_gather(const void* V, int v_dtype,
@@ -226,6 +228,21 @@ int t2t_tile_attn_exact_orig_gather(const void* q, const void* k, const int32_t*
                                     const void* vp, int dtype, const int32_t* kcounts,
                                     const int32_t* unip, const int32_t* qperm, const int32_t* plan,
                                     void* out, float* lse, int H, int N, int CQ, void* stream);
+/* t2t_tile_attn_exact_orig_gather with the V gather fused as well: v is
+ * [H, N, 128] in the ORIGINAL order and key position p reads row kperm[h, p]
+ * of both k and v, so neither kp nor V_sorted is stored.  All tensors are
+ * strided [H, N, 128] views as for the strided entry points below (one
+ * head's K and V rows must each span under 4 GiB).  Replaces the
+ * fast_gather of K and the V_sorted of kmm_ext.run / run_vstats_gather
+ * (deploy_step.py:326,456; kmeans_maintain/src/kernels.cu:900-923) together
+ * with the attention launch that reads them (tile_attn/src/kernel.cu:820-1096). */
+int t2t_tile_attn_exact_orig_gather_kv_strided(
+    const void* q, long long q_head_stride, long long q_row_stride, const void* k,
+    long long k_head_stride, long long k_row_stride, const void* v, long long v_head_stride,
+    long long v_row_stride, const int32_t* kperm, int dtype, const int32_t* kcounts,
+    const int32_t* unip, const int32_t* qperm, const int32_t* plan, void* out,
+    long long out_head_stride, long long out_row_stride, float* lse, int H, int N, int CQ,
+    void* stream);
 /* ---- strided variants ---------------------------------------------------
  * No counterpart in the reference: its SGLang backend copies q, k and v from
  * the model's token-major [1, N, H, 128] into head-major [H, N, 128] and the

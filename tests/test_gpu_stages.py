@@ -377,6 +377,16 @@ def test_exact_orig_gather_equals_gathered(dev, dtype):
     ops.tile_attn_exact_orig_gather(tq, tk, g(kperm, dev), tvp, *args, out_b, lse_b)
     assert torch.equal(out_a, out_b) and torch.equal(lse_a, lse_b)
     assert int(kcounts.min()) == 0  # the case holds empty key clusters
+    # V read through kperm as well (original-order v, also as token-major views)
+    out_c, lse_c = torch.zeros_like(tq), torch.zeros(H, N, dtype=torch.float32, device=dev)
+    tv = g(v, dev).to(dtype)
+    ops.tile_attn_exact_orig_gather_kv(tq, tk, tv, g(kperm, dev), *args, out_c, lse_c)
+    assert torch.equal(out_a, out_c) and torch.equal(lse_a, lse_c)
+    qm, km, vm = (t.transpose(0, 1).contiguous().transpose(0, 1) for t in (tq, tk, tv))
+    om = torch.zeros(N, H, 128, dtype=dtype, device=dev)
+    lse_d = torch.zeros(H, N, dtype=torch.float32, device=dev)
+    ops.tile_attn_exact_orig_gather_kv(qm, km, vm, g(kperm, dev), *args, om.transpose(0, 1), lse_d)
+    assert torch.equal(out_a, om.transpose(0, 1)) and torch.equal(lse_a, lse_d)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

@@ -132,6 +132,31 @@ def test_fused_k_gather_is_bit_identical(dev, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_v_gather_is_bit_identical(dev, dtype):
+    """V read through kperm by the attention kernel (no V_sorted; the value
+    statistics of a reuse call on the side stream) gives the same bits as the
+    V_sorted path, on a full call and a reuse call with a new V."""
+    deploy, q, k, v = make(dev, mask_refresh=4)
+    tq, tk, tv = (torch.from_numpy(a).to(dev).to(dtype) for a in (q, k, v))
+    tv2 = (tv.float() * 0.5 + 0.25).to(dtype)
+    state = deploy.init_state(tq, tk, seed=4)
+    outs = {}
+    for fused in (True, False):
+        deploy.fuse_v_gather = fused
+        st = {k_: v_.clone() for k_, v_ in state.items()}
+        deploy.reset_cfg_reuse()
+        deploy.set_cfg_call(0, key=1, step=0)
+        full = deploy.step(tq, tk, tv, st).clone()
+        deploy.set_cfg_call(1, key=1, step=0)
+        reuse = deploy.step(tq, tk, tv2, st).clone()
+        assert not deploy.last_call_full
+        outs[fused] = (full, reuse)
+    deploy.fuse_v_gather = True
+    assert torch.equal(outs[True][0], outs[False][0])
+    assert torch.equal(outs[True][1], outs[False][1])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_token_major_views_are_bit_identical(dev, dtype):
     """q, k, v given as token-major [N, H, 128] tensors seen through
     .transpose(0, 1), with the output written into a token-major view: the

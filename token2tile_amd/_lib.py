@@ -56,6 +56,11 @@ SIGNATURES = {
                                          c_int, _P]),
     "t2t_tile_attn_exact_orig_gather": (c_int, [_P, _P, _P, _P, c_int, _P, _P, _P, _P, _P, _P,
                                                 c_int, c_int, c_int, _P]),
+    "t2t_tile_attn_exact_orig_gather_kv_strided": (c_int, [_P, c_longlong, c_longlong, _P, c_longlong,
+                                                           c_longlong, _P, c_longlong, c_longlong,
+                                                           _P, c_int, _P, _P, _P, _P, _P,
+                                                           c_longlong, c_longlong, _P, c_int,
+                                                           c_int, c_int, _P]),
     "t2t_project_strided": (c_int, [_P, c_int, _P, _P, c_int, c_int, c_int, c_int, c_longlong,
                                     c_longlong, _P]),
     "t2t_kmm_run_strided": (c_int, [_P, _P, _P, c_int, c_longlong, c_longlong] + [_P] * 13 +

@@ -273,6 +273,8 @@ __device__ inline uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_am
 // MODE 1: the exact output at the original rows of out, lse in sorted order
 // MODE 2: as MODE 1, with the K gather fused: kp is k in its original order and
 // key position p of cluster order reads row kperm[p] (no separate kp = k[kperm])
+// MODE 3: as MODE 2, with the V gather fused as well: vp is v in its original
+// order, read through kperm like K (no V_sorted)
 // (the residual kernel merges into out in place).
 template <typename T, int MODE>
 __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
@@ -282,10 +284,12 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     const int32_t* __restrict__ k_off, const int32_t* __restrict__ ntask,
     const int32_t* __restrict__ tasks, uint16_t* __restrict__ attn_out, float* __restrict__ lse,
     uint16_t* __restrict__ out, const int32_t* __restrict__ kperm, int H, int N, int CQ, int maxT,
-    long long sqh, long long sqn, long long skh, long long skn, long long soh, long long son) {
+    long long sqh, long long sqn, long long skh, long long skn, long long soh, long long son,
+    long long svh, long long svn) {
   // row n of head h of q / k (MODE 2) / out (MODE 1, 2) sits at base + h s_h + n s_n
   // (elements): [H, N, 128] contiguous or a strided view such as token-major [N, H, 128]
-  constexpr bool KG = MODE == 2;
+  constexpr bool KG = MODE >= 2;
+  constexpr bool VG = MODE == 3;
   // two separate arrays (not one [2][...] array): the K DMA into one buffer
   // must not be taken as a possible writer of the other one, or every read of
   // the tile in use would wait for the loads of the tile in flight
@@ -454,7 +458,8 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     // byte offsets of K rows from the head base stay 32-bit (the entry point
     // checks (N - 1) * row stride fits): 64-bit address math here cost 3.6%
     const uint32_t krow_bytes = KG ? (uint32_t)(skn * 2) : 256u;
-    const char* vh = (const char*)(vp + (size_t)h * N * TA_D);
+    const char* vh = (const char*)(vp + (VG ? (size_t)h * svh : (size_t)h * N * TA_D));
+    const uint32_t vrow_bytes = VG ? (uint32_t)(svn * 2) : 256u;
     const int ntile = (kvlen + TA_KT - 1) / TA_KT;
     // source rows of tile `tile` -> sIdx[tile & 1]; past the end -> row 0
     // (its keys are masked and its values multiply a zero probability).
@@ -515,7 +520,8 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
         const uint32_t base = (uint32_t)sIdx[buf][row] * 256u;
         const uint32_t kbase = KG ? (uint32_t)sIdxK[buf][row] * krow_bytes : base;
         const uint32_t offk = kbase + 16u * ((lane & 15) ^ (row & 15));
-        const uint32_t offv = base + 16u * ((lane & 15) ^ sv_swz(row));
+        const uint32_t vbase = VG ? (uint32_t)sIdxK[buf][row] * vrow_bytes : base;
+        const uint32_t offv = vbase + 16u * ((lane & 15) ^ sv_swz(row));
         __builtin_amdgcn_global_load_lds((const glb_void_t*)(kh + offk),
                                          (lds_void_t*)(sKb + blk * 4 * 128), 16, 0, 0);
         __builtin_amdgcn_global_load_lds((const glb_void_t*)(vh + offv),
@@ -670,9 +676,11 @@ static void launch_attn(const void* q, const void* kp, const void* vp, const int
                         void* attn_out, float* lse, void* out, int H, int N, int CQ,
                         hipStream_t st, const int32_t* kperm = nullptr, long long sqh = -1,
                         long long sqn = TA_D, long long skh = -1, long long skn = TA_D,
-                        long long soh = -1, long long son = TA_D) {
+                        long long soh = -1, long long son = TA_D, long long svh = -1,
+                        long long svn = TA_D) {
   // default strides: [H, N, 128] contiguous
   if (sqh < 0) sqh = (long long)N * TA_D;
+  if (svh < 0) svh = (long long)N * TA_D;
   if (skh < 0) skh = (long long)N * TA_D;
   if (soh < 0) soh = (long long)N * TA_D;
   const int total = H * p.maxT;
@@ -681,7 +689,7 @@ static void launch_attn(const void* q, const void* kp, const void* vp, const int
                      (const uint16_t*)q, (const uint16_t*)kp, (const uint16_t*)vp,
                      (const uint32_t*)unip, qperm, kcounts, p.k_off, p.ntask, p.tasks,
                      (uint16_t*)attn_out, lse, (uint16_t*)out, kperm, H, N, CQ, p.maxT, sqh, sqn,
-                     skh, skn, soh, son);
+                     skh, skn, soh, son, svh, svn);
 }
 
 // ---------------------------------------------------------------------------
@@ -1067,6 +1075,42 @@ extern "C" int t2t_tile_attn_exact_orig_gather_strided(
   return exact_gather_impl(q, q_head_stride, q_row_stride, k, k_head_stride, k_row_stride, kperm,
                            vp, dtype, kcounts, unip, qperm, plan, out, out_head_stride,
                            out_row_stride, lse, H, N, CQ, stream);
+}
+
+extern "C" int t2t_tile_attn_exact_orig_gather_kv_strided(
+    const void* q, long long q_head_stride, long long q_row_stride, const void* k,
+    long long k_head_stride, long long k_row_stride, const void* v, long long v_head_stride,
+    long long v_row_stride, const int32_t* kperm, int dtype, const int32_t* kcounts,
+    const int32_t* unip, const int32_t* qperm, const int32_t* plan, void* out,
+    long long out_head_stride, long long out_row_stride, float* lse, int H, int N, int CQ,
+    void* stream) {
+  T2T_REQUIRE(q && k && v && kperm && kcounts && unip && qperm && plan && out && lse,
+              "tile_attn_exact_orig_gather_kv: null pointer");
+  T2T_REQUIRE(check_dtype(dtype), "tile_attn_exact_orig_gather_kv: dtype %d", dtype);
+  T2T_REQUIRE(H > 0 && N > 0 && N < (1 << 24) && CQ > 0,
+              "tile_attn_exact_orig_gather_kv: H=%d N=%d CQ=%d", H, N, CQ);
+  const long long st4[8] = {q_head_stride, q_row_stride, k_head_stride, k_row_stride,
+                            v_head_stride, v_row_stride, out_head_stride, out_row_stride};
+  for (int i = 0; i < 8; ++i)
+    T2T_REQUIRE(st4[i] >= 0 && st4[i] % 8 == 0 && (i % 2 == 0 || st4[i] >= TA_D),
+                "tile_attn_exact_orig_gather_kv: strides must be non-negative multiples of 8 "
+                "elements with row strides >= 128");
+  for (long long rs : {k_row_stride, v_row_stride})
+    T2T_REQUIRE((unsigned long long)(N - 1) * (unsigned long long)rs * 2ull + 256ull <= 0xFFFFFFFFull,
+                "tile_attn_exact_orig_gather_kv: one head's K or V rows span (N - 1) * %lld "
+                "elements, more than 4 GiB", rs);
+  PlanView p = plan_view((int32_t*)plan, H, N, CQ);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == T2T_F16)
+    launch_attn<F16T, 3>(q, k, v, unip, qperm, kcounts, p, nullptr, lse, out, H, N, CQ, st, kperm,
+                         q_head_stride, q_row_stride, k_head_stride, k_row_stride, out_head_stride,
+                         out_row_stride, v_head_stride, v_row_stride);
+  else
+    launch_attn<BF16T, 3>(q, k, v, unip, qperm, kcounts, p, nullptr, lse, out, H, N, CQ, st, kperm,
+                          q_head_stride, q_row_stride, k_head_stride, k_row_stride,
+                          out_head_stride, out_row_stride, v_head_stride, v_row_stride);
+  T2T_LAUNCH_CHECK("tile_attn_exact_orig_gather_kv");
+  return T2T_OK;
 }
 
 extern "C" int t2t_tile_attn_exact_orig(const void* q, const void* kp, const void* vp, int dtype,

@@ -174,6 +174,10 @@ class MaskedStepDeploy:
         # the exact-attention kernel reads K through kperm (kp = k[kperm] is
         # not materialised); False restores the reference's separate gather
         self.fuse_k_gather = True
+        # ... and V through kperm too, so V_sorted is not materialised either;
+        # the value statistics of a reuse call then run on s_side beside the
+        # exact attention.  False restores the V_sorted buffer
+        self.fuse_v_gather = True
         self._kmm_cq2 = torch.empty(H, CQ, r, device=dev, dtype=f16)
         self._kmm_ck2 = torch.empty(H, C, r, device=dev, dtype=f32)
         self._kmm_kcounts = torch.empty(H, C, device=dev, dtype=i32)
@@ -225,8 +229,8 @@ class MaskedStepDeploy:
         io = self._io.get(dtype)
         if io is None:
             H, N, D = self.H, self.N, self.D
-            io = dict(kp=None,  # allocated on first use (the fused gather needs none)
-                      vp=torch.empty(H, N, D, device=self.dev, dtype=dtype),
+            # kp and vp are allocated on first use: the fused gathers need neither
+            io = dict(kp=None, vp=None,
                       out=torch.empty(H, N, D, device=self.dev, dtype=dtype),
                       attn_out=None, lse=None)
             self._io[dtype] = io
@@ -244,9 +248,21 @@ class MaskedStepDeploy:
         ``fuse_k_gather`` is off (the fused kernel reads k through kperm)."""
         return self._kp(torch.float16)
 
+    def _vp(self, dtype):
+        io = self._buffers(dtype)
+        if io["vp"] is None:
+            io["vp"] = torch.empty(self.H, self.N, self.D, device=self.dev, dtype=dtype)
+        return io["vp"]
+
     @property
     def vp(self):
-        return self._buffers(torch.float16)["vp"]
+        """The cluster-ordered V buffer (V_sorted); written by ``step`` only
+        when a gather is unfused (the fused kernel reads v through kperm)."""
+        return self._vp(torch.float16)
+
+    @property
+    def _fused_kv(self):
+        return self.fuse_k_gather and self.fuse_v_gather
 
     # -- state init (deploy_step.py:245-266) ---------------------------------
     def init_state(self, q, k, *, warm_iters=4, seed=0):
@@ -343,20 +359,26 @@ class MaskedStepDeploy:
             if snap is not None:
                 # reuse: project with the snapshot's Uq, group K and V through
                 # the stored kperm, fresh value statistics from this call's V.
-                # Only the residual reads QU, so the projection runs on the
-                # side stream, under the V statistics and the exact attention.
+                # Only the residual reads QU, sumv and lam: with the fused
+                # gathers the projection and the value statistics run on the
+                # side stream, under the exact attention.
                 s1.wait_stream(s0)
                 ops.project(q, snap["Uq"], out=self.QU, stream=s1)
+                if self._fused_kv:
+                    ops.vstats_gather(v, snap["kperm"], snap["counts"], sumv=self._kmm_sumv,
+                                      lam=self._kmm_lam, ws=self._ws_vst, stream=s1,
+                                      write_v_sorted=False)
                 qu_ready = torch.cuda.Event()
                 qu_ready.record(s1)
                 if not self.fuse_k_gather:
                     with self._stage("gather_k"):
                         ops.fast_gather(k, snap["kperm"], out=self._kp(k.dtype), stream=s0)
                 kperm = snap["kperm"]
-                with self._stage("vstats"):
-                    ops.vstats_gather(v, snap["kperm"], snap["counts"], V_sorted=io["vp"],
-                                      sumv=self._kmm_sumv, lam=self._kmm_lam, ws=self._ws_vst,
-                                      stream=s0)
+                if not self._fused_kv:
+                    with self._stage("vstats"):
+                        ops.vstats_gather(v, snap["kperm"], snap["counts"],
+                                          V_sorted=self._vp(v.dtype), sumv=self._kmm_sumv,
+                                          lam=self._kmm_lam, ws=self._ws_vst, stream=s0)
                 tile_sizes, qperm, counts = snap["tile_sizes"], snap["qperm"], snap["counts"]
                 qlab_cur, cks, unip = snap["qlab"], snap["cks"], snap["unip"]
                 plan, rebuild = snap["tile_attn_plan"], False
@@ -374,11 +396,14 @@ class MaskedStepDeploy:
                                   qperm=torch.empty(H, N, device=self.dev, dtype=torch.int32),
                                   kperm=torch.empty(H, N, device=self.dev, dtype=torch.int32),
                                   kcounts=self._kmm_kcounts)
-                km_out.update(cq2=self._kmm_cq2, ck2=self._kmm_ck2, V_sorted=io["vp"],
-                              sumv=self._kmm_sumv, lam=self._kmm_lam)
+                km_out.update(cq2=self._kmm_cq2, ck2=self._kmm_ck2, sumv=self._kmm_sumv,
+                              lam=self._kmm_lam)
+                if not self._fused_kv:
+                    km_out.update(V_sorted=self._vp(v.dtype))
                 with self._stage("kmeans"):
                     ops.kmm_run(self.QU, self.KU, v, state["cq"], state["ck"],
-                                pin_tail=self.pin_tail, out=km_out, ws=self._ws_kmm, stream=s0)
+                                pin_tail=self.pin_tail, out=km_out, ws=self._ws_kmm, stream=s0,
+                                write_v_sorted=not self._fused_kv)
                 tile_sizes, qperm, counts = km_out["qcounts"], km_out["qperm"], km_out["kcounts"]
                 with self._stage("score"):
                     ck16, cks = ops.centroid_finalize(self._kmm_ck2, self.scale, stream=s0)
@@ -423,17 +448,22 @@ class MaskedStepDeploy:
                 with self._stage("plan"):
                     ops.tile_plan(tile_sizes, counts, unip, N, plan=plan, stream=s0)
             # the steps of t2t_tile_attn_run_planned, one launch per stage
-            with self._stage("attention_prep"):
-                ops.centroid_tiles(cks, self._kmm_sumv, tiles=self._ctiles, stream=s0)
+            # (the centroid tile image after the side stream's value
+            # statistics on reuse calls)
             with self._stage("attention_exact"):
-                if self.fuse_k_gather:
-                    ops.tile_attn_exact_orig_gather(q, k, kperm, io["vp"], counts, unip, qperm, plan,
-                                                    dst, self._lse, stream=s0)
+                if self._fused_kv:
+                    ops.tile_attn_exact_orig_gather_kv(q, k, v, kperm, counts, unip, qperm, plan,
+                                                       dst, self._lse, stream=s0)
+                elif self.fuse_k_gather:
+                    ops.tile_attn_exact_orig_gather(q, k, kperm, self._vp(v.dtype), counts, unip,
+                                                    qperm, plan, dst, self._lse, stream=s0)
                 else:
-                    ops.tile_attn_exact_orig(q, io["kp"], io["vp"], counts, unip, qperm, plan,
-                                             dst, self._lse, stream=s0)
+                    ops.tile_attn_exact_orig(q, io["kp"], self._vp(v.dtype), counts, unip, qperm,
+                                             plan, dst, self._lse, stream=s0)
             if qu_ready is not None:
                 s0.wait_event(qu_ready)
+            with self._stage("attention_prep"):
+                ops.centroid_tiles(cks, self._kmm_sumv, tiles=self._ctiles, stream=s0)
             with self._stage("attention_residual"):
                 ops.resid_merge_inplace(dst, self._lse, self.QU, self._ctiles, counts, unip,
                                         qlab_cur, qperm, self._kmm_lam, self.tailw_t, stream=s0)

@@ -112,8 +112,11 @@ def kmm_ws_bytes(H, N, CQ, CK=C_KEYS):
     return size_query("t2t_kmm_ws_bytes", H, N, CQ, CK)
 
 
-def kmm_run(QU, KU, V, cq0, ck0, *, pin_tail=0, out=None, ws=None, stream=None):
-    """One k-means maintenance call; returns a dict of the outputs."""
+def kmm_run(QU, KU, V, cq0, ck0, *, pin_tail=0, out=None, ws=None, stream=None,
+            write_v_sorted=True):
+    """One k-means maintenance call; returns a dict of the outputs.  With
+    ``write_v_sorted=False`` V_sorted is neither allocated nor written (its
+    entry is None): for callers that read V through kperm."""
     H, N, r = QU.shape
     CQ, CK = cq0.shape[1], ck0.shape[1]
     dev = _dev(QU)
@@ -131,7 +134,10 @@ def kmm_run(QU, KU, V, cq0, ck0, *, pin_tail=0, out=None, ws=None, stream=None):
     o.setdefault("qperm", torch.empty(H, N, dtype=_i32, device=dev))
     o.setdefault("kcounts", torch.empty(H, CK, dtype=_i32, device=dev))
     o.setdefault("kperm", torch.empty(H, N, dtype=_i32, device=dev))
-    o.setdefault("V_sorted", torch.empty(H, N, HEAD_DIM, dtype=V.dtype, device=dev))
+    if write_v_sorted:
+        o.setdefault("V_sorted", torch.empty(H, N, HEAD_DIM, dtype=V.dtype, device=dev))
+    else:
+        o["V_sorted"] = None
     o.setdefault("sumv", torch.empty(H, CK, HEAD_DIM, dtype=_f16, device=dev))
     o.setdefault("lam", torch.empty(H, dtype=_f32, device=dev))
     for name, shape, dt in (("qlab", (H, N), _i32), ("cq2", (H, CQ, r), _f16),
@@ -140,7 +146,8 @@ def kmm_run(QU, KU, V, cq0, ck0, *, pin_tail=0, out=None, ws=None, stream=None):
                             ("kcounts", (H, CK), _i32), ("kperm", (H, N), _i32),
                             ("V_sorted", (H, N, HEAD_DIM), V.dtype),
                             ("sumv", (H, CK, HEAD_DIM), _f16), ("lam", (H,), _f32)):
-        _check(o[name], shape, dt, name, dev)
+        if o[name] is not None or name != "V_sorted":
+            _check(o[name], shape, dt, name, dev)
     need = kmm_ws_bytes(H, N, CQ, CK)
     ws = _ws_for(ws, need, dev)
     if V.is_contiguous():
@@ -161,19 +168,24 @@ def vstats_ws_bytes(H, N, CK=C_KEYS):
     return size_query("t2t_vstats_ws_bytes", H, N, CK)
 
 
-def vstats_gather(V, kperm, kcounts, V_sorted=None, sumv=None, lam=None, ws=None, stream=None):
-    """Reuse-call value statistics: V_sorted = V[kperm], sumv, lam."""
+def vstats_gather(V, kperm, kcounts, V_sorted=None, sumv=None, lam=None, ws=None, stream=None,
+                  write_v_sorted=True):
+    """Reuse-call value statistics: V_sorted = V[kperm], sumv, lam.  With
+    ``write_v_sorted=False`` only sumv and lam are produced (V_sorted None)."""
     H, N, D = V.shape
     CK = kcounts.shape[1]
     dev = _dev(V)
-    V_sorted = (torch.empty(H, N, D, dtype=V.dtype, device=dev) if V_sorted is None
-                else V_sorted)
+    if not write_v_sorted:
+        V_sorted = None
+    elif V_sorted is None:
+        V_sorted = torch.empty(H, N, D, dtype=V.dtype, device=dev)
     sumv = torch.empty(H, CK, D, dtype=_f16, device=dev) if sumv is None else sumv
     lam = torch.empty(H, dtype=_f32, device=dev) if lam is None else lam
     svh, svn = _rows(V, H, N, HEAD_DIM, _HALF, "V", dev)
     _check(kperm, (H, N), _i32, "kperm", dev)
     _check(kcounts, (H, CK), _i32, "kcounts", dev)
-    _check(V_sorted, (H, N, HEAD_DIM), V.dtype, "V_sorted", dev)
+    if V_sorted is not None:
+        _check(V_sorted, (H, N, HEAD_DIM), V.dtype, "V_sorted", dev)
     _check(sumv, (H, CK, HEAD_DIM), _f16, "sumv", dev)
     _check(lam, (H,), _f32, "lam", dev)
     need = vstats_ws_bytes(H, N, CK)
@@ -458,6 +470,28 @@ def tile_attn_exact_orig_gather(q, k, kperm, vp, kcounts, unip, qperm, plan, out
              *sk, kperm, vp, dtype_code(q.dtype), kcounts, unip, qperm, plan, _lib.RowView(out),
              *so, lse, H, N, CQ, stream_handle(stream))
     return out
+
+def tile_attn_exact_orig_gather_kv(q, k, v, kperm, kcounts, unip, qperm, plan, out, lse,
+                                   stream=None):
+    """Exact attention with both gathers fused: k and v in the original order,
+    key position p of the cluster order at row kperm[h, p] of each (neither
+    kp nor V_sorted is stored).  q, k, v and out may be strided [H, N, 128]
+    views with contiguous rows."""
+    H, N, D = q.shape
+    CQ = unip.shape[1]
+    dev = _dev(q)
+    sq = _rows(q, H, N, HEAD_DIM, _HALF, "q", dev)
+    sk = _rows(k, H, N, HEAD_DIM, q.dtype, "k", dev)
+    sv = _rows(v, H, N, HEAD_DIM, q.dtype, "v", dev)
+    so = _rows(out, H, N, HEAD_DIM, q.dtype, "out", dev)
+    _check_attn(dev, H, N, CQ, kcounts=kcounts, unip=unip, qperm=qperm, plan=plan, lse=lse,
+                dt=q.dtype)
+    _check(kperm, (H, N), _i32, "kperm", dev)
+    call("t2t_tile_attn_exact_orig_gather_kv_strided", _lib.RowView(q), *sq, _lib.RowView(k), *sk,
+         _lib.RowView(v), *sv, kperm, dtype_code(q.dtype), kcounts, unip, qperm, plan,
+         _lib.RowView(out), *so, lse, H, N, CQ, stream_handle(stream))
+    return out
+
 
 def resid_merge_inplace(out, lse, QU, tiles, kcounts, unip, qlab, qperm, lam, tailw_t,
                         stream=None):
