@@ -76,3 +76,65 @@ def test_h3_layout_record_drives_the_varlen_rules():
 def test_resolver_on_this_device(dev):
     assert S.device_arch() == "gfx950"
     assert S.resolve_backend() == S.BACKEND_PATH
+
+
+def _old_side(patch_text):
+    """Files holding each hunk's old-side lines at the hunk's old start line
+    (filler elsewhere): enough for `git apply` to check the hunk headers."""
+    import re
+    files, cur = {}, None
+    lines = patch_text.splitlines()
+    i = 0
+    while i < len(lines):
+        ln = lines[i]
+        if ln.startswith("--- a/"):
+            cur = ln[6:]
+            files.setdefault(cur, {})
+        m = re.match(r"@@ -(\d+),(\d+) \+\d+,\d+ @@", ln)
+        if m:
+            at, n = int(m.group(1)), int(m.group(2))
+            i += 1
+            while n:
+                body = lines[i]
+                if body[:1] in (" ", "-") or body == "":
+                    files[cur][at] = body[1:]
+                    at += 1
+                    n -= 1
+                i += 1
+            continue
+        i += 1
+    out = {}
+    for path, rows in files.items():
+        last = max(rows) + 5
+        out[path] = "\n".join(rows.get(r, f"# filler {r}") for r in range(1, last + 1)) + "\n"
+    return out
+
+
+def test_rocm_patch_applies_and_calls_existing_hooks(tmp_path):
+    """The ROCm patch beside the backend parses, applies hunk-for-hunk to its
+    own context, adds the T2T_ATTN enum member the backend's get_enum names,
+    and only calls hooks this module defines."""
+    import pathlib
+    import re
+    import subprocess
+    root = pathlib.Path(S.__file__).parent / "sglang"
+    patch = root / "token2tile_rocm.patch"
+    text = patch.read_text()
+    for path, body in _old_side(text).items():
+        f = tmp_path / path
+        f.parent.mkdir(parents=True, exist_ok=True)
+        f.write_text(body)
+    subprocess.run(["git", "init", "-q", str(tmp_path)], check=True)
+    subprocess.run(["git", "-C", str(tmp_path), "apply", str(patch)], check=True)
+    iface = (tmp_path / "python/sglang/multimodal_gen/runtime/platforms/interface.py").read_text()
+    assert "    T2T_ATTN = enum.auto()" in iface
+    assert getattr(B.T2TAttentionBackend.get_enum(), "name", "T2T_ATTN") == "T2T_ATTN"
+    assert B.AttentionBackendEnum.T2T_ATTN is B.T2TAttentionBackend.get_enum()
+    called = set(re.findall(r"from token2tile_amd\.backend\.sglang_hooks import (\w+)", text))
+    assert called == {"build_denoising_metadata", "minimax_h3_layout"}
+    for name in called:
+        assert callable(getattr(S, name))
+    # the apply script pins the SGLang commit the context lines come from
+    script = (root / "apply.sh").read_text()
+    assert "880ab72f34ead8f39544c7c7e08edbd443964a1f" in script
+    assert "token2tile_rocm.patch" in script
