@@ -239,6 +239,41 @@ def test_kmeans_labels_near_ties_only_and_chained_exact(dev):
     assert np.array_equal(c(o["qperm"]), qperm) and np.array_equal(c(o["qcounts"]), qcounts)
 
 
+def test_kmeans_labels_do_not_depend_on_label_buffer_contents(dev):
+    """The assignment starts its running minimum from the label buffers' old
+    contents (a guess plus a rounding bound); every output must be the same
+    whatever those contents are: unset, the exact answer, wrong labels, or
+    the higher index of duplicated centroids (exact ties -> lowest index)."""
+    from token2tile_amd import ops
+    rng = np.random.default_rng(41)
+    H, N, CQ, CK = 2, 5000, 96, 2048
+    QU = rng.normal(0, 1, (H, N, 32)).astype(np.float16)
+    KU = rng.normal(0, 1, (H, N, 32)).astype(np.float16)
+    cq0 = QU[:, rng.choice(N, CQ, replace=False)].copy()
+    ck0 = KU[:, rng.choice(N, CK, replace=False)].copy()
+    ck0[:, 1500] = ck0[:, 7]                                 # exact ties: 7 must win
+    cq0[:, 90] = cq0[:, 3]
+    V = rng.normal(0, 1, (H, N, 128)).astype(np.float16)
+    args = [g(a, dev) for a in (QU, KU, V, cq0, ck0)]
+
+    def run(qlab0, klab0):
+        out = {"qlab": g(qlab0.astype(np.int32), dev), "klab": g(klab0.astype(np.int32), dev)}
+        o = ops.kmm_run(*args, out=out)
+        return {k_: c(v_) for k_, v_ in o.items() if v_ is not None}
+
+    base = run(np.full((H, N), -1), np.full((H, N), -1))
+    exact_q, exact_k = base["qlab"], base["klab"]
+    swap = lambda lab, a, b: np.where(lab == a, b, lab)   # noqa: E731
+    for qg, kg in ((exact_q, exact_k),
+                   ((exact_q + 1) % CQ, (exact_k + 5) % CK),
+                   (swap(exact_q, 3, 90), swap(exact_k, 7, 1500)),
+                   (rng.integers(-50, CQ + 50, (H, N)), rng.integers(-50, CK + 50, (H, N)))):
+        o = run(qg, kg)
+        for k_ in base:
+            assert np.array_equal(o[k_], base[k_]), k_
+    assert not np.any(exact_k == 1500) and np.any(exact_k == 7)
+
+
 def test_vstats_reuse_paths(dev):
     from token2tile_amd import ops
     rng = np.random.default_rng(5)
@@ -314,8 +349,21 @@ def test_plan(dev):
             assert 1 <= rows <= 128 and qoff[h, t] <= s and s + rows <= qoff[h, t] + qcounts[h, t]
             covered[s:s + rows] += 1
         assert np.all(covered == 1)
-        work = tasks[:, 2].astype(np.int64) * kvlen[h, tasks[:, 0]]
+        # whole waves of 32 queries: a cluster's tasks use ceil(n / 32) waves in
+        # ceil(n / 128) tasks (only the last task of a cluster has a partial wave)
+        for t in np.unique(tasks[:, 0]):
+            rows = tasks[tasks[:, 0] == t, 2]
+            n = qcounts[h, t]
+            assert len(rows) == -(-n // 128)
+            assert (-(-rows // 32)).sum() == -(-n // 32)
+        # LPT by the cluster's largest task; a cluster's tasks are adjacent
+        work = tasks[:, 3].astype(np.int64) * kvlen[h, tasks[:, 0]]
         assert np.all(np.diff(work) <= 0)
+        assert np.all(tasks[:, 2] <= tasks[:, 3])
+        first = {}
+        for i, t in enumerate(tasks[:, 0]):
+            first.setdefault(t, i)
+            assert i - first[t] < -(-qcounts[h, t] // 128)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

@@ -30,7 +30,8 @@ __global__ __launch_bounds__(256) void assign_kernel(const uint16_t* __restrict_
                                                      const uint16_t* __restrict__ cprep,
                                                      const float* __restrict__ cnorm,
                                                      int32_t* __restrict__ labels, int N, int C,
-                                                     int pin_begin, int pin_label, int ibits) {
+                                                     int pin_begin, int pin_label, int ibits,
+                                                     const int32_t* __restrict__ guess) {
   constexpr int KS = D / 16;
   __shared__ __attribute__((aligned(16))) uint16_t sC[AS_CHUNK * D];
   __shared__ float sN[AS_CHUNK];
@@ -60,6 +61,44 @@ __global__ __launch_bounds__(256) void assign_kernel(const uint16_t* __restrict_
   float best = __builtin_inff();
   int bidx = 0;
   int bkey = 0x7fffffff;
+  // MODE 0 pruning bound from a guess: the row's previous label (any value;
+  // used only when it names a centroid).  Its distance, summed here in fp32,
+  // plus a bound on the rounding of that sum and of the MFMA's own (33 terms
+  // in any order: under 2^-18 of the sum of their magnitudes each; 2^-16 is
+  // taken) is strictly above the MFMA distance of the guessed centroid, so
+  // starting the running minimum there changes no label: the result is still
+  // the first centroid, in visiting order, at the minimum MFMA distance.  It
+  // only spares the index search of every block that cannot hold that minimum.
+  if (MODE == 0 && guess && cprep) {
+    const int g = ok ? guess[(size_t)h * N + row] : -1;
+    const bool have = g >= 0 && g < C;
+    float part = 0.f, mag = 0.f;
+    if (have) {
+      const uint16_t* cg = cprep + ((size_t)h * C + g) * D;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4 cv = *(const u32x4*)(cg + 16 * s + 8 * hh);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float x0 = h2f((uint16_t)(bx[s][t] & 0xffff)), c0 = h2f((uint16_t)(cv[t] & 0xffff));
+          const float x1 = h2f((uint16_t)(bx[s][t] >> 16)), c1 = h2f((uint16_t)(cv[t] >> 16));
+          part = fmaf(x0, c0, part);
+          part = fmaf(x1, c1, part);
+          mag = fmaf(fabsf(x0), fabsf(c0), mag);
+          mag = fmaf(fabsf(x1), fabsf(c1), mag);
+        }
+      }
+    }
+    const float opart = __builtin_bit_cast(float, half_partner(__builtin_bit_cast(uint32_t, part)));
+    const float omag = __builtin_bit_cast(float, half_partner(__builtin_bit_cast(uint32_t, mag)));
+    if (have) {
+      const float cn = cnorm[(size_t)h * C + g];
+      const float d = cn + (hh ? opart + part : part + opart);
+      const float sz = fabsf(cn) + (hh ? omag + mag : mag + omag);
+      best = d + 0x1p-16f * sz + 0x1p-126f;
+      bidx = g;
+    }
+  }
   const int kmask = -(1 << ibits);
   for (int c0 = 0; c0 < Cp; c0 += AS_CHUNK) {
     const int nc = (Cp - c0) < AS_CHUNK ? (Cp - c0) : AS_CHUNK;
@@ -118,15 +157,31 @@ __global__ __launch_bounds__(256) void assign_kernel(const uint16_t* __restrict_
         const u32x4 av = *(const u32x4*)(sC + (cb * 32 + jl) * D + 16 * s + 8 * hh);
         acc = Mfma<F16T>::run(av, bx[s], acc);
       }
+      if (MODE == 0) {
+        // the block's minimum by a min3 tree; only a block that improves some
+        // lane's running minimum looks for its lowest index at that value
+        // (accumulator order a is ascending centroid order)
+        auto mn = [](float a, float b) { return __builtin_elementwise_minimum(a, b); };
+        float t8[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t8[i] = mn(acc[2 * i], acc[2 * i + 1]);
+        const float bmin = mn(mn(mn(t8[0], t8[1]), mn(t8[2], t8[3])),
+                              mn(mn(t8[4], t8[5]), mn(t8[6], t8[7])));
+        if (__ballot(bmin < best) != 0ull) {
+          if (bmin < best) {
+            int ia = 15;
+#pragma unroll
+            for (int a = 14; a >= 0; --a) ia = acc[a] == bmin ? a : ia;
+            best = bmin;
+            bidx = c0 + cb * 32 + 8 * (ia >> 2) + 4 * hh + (ia & 3);
+          }
+        }
+        continue;
+      }
 #pragma unroll
       for (int a = 0; a < 16; ++a) {
         const int ci = c0 + cb * 32 + 8 * (a / 4) + 4 * hh + (a % 4);
-        if (MODE == 0) {
-          if (acc[a] < best) {
-            best = acc[a];
-            bidx = ci;
-          }
-        } else {
+        {
           const float cn2 = sN[cb * 32 + 8 * (a / 4) + 4 * hh + (a % 4)];
           const float d2 = xsq + (cn2 - 2.0f * acc[a]);
           int key = (__builtin_bit_cast(int, d2) & kmask) | ci;
@@ -546,12 +601,12 @@ __global__ __launch_bounds__(256) void cen_prep_kernel(const uint16_t* __restric
 
 static int launch_assign_km(const void* X, const void* cen, int32_t* lab, int H, int N, int C,
                             int pin_begin, int pin_label, uint16_t* cprep, float* cnorm,
-                            hipStream_t st) {
+                            const int32_t* guess, hipStream_t st) {
   hipLaunchKernelGGL(cen_prep_kernel, dim3(cdiv(C, 256), H), dim3(256), 0, st,
                      (const uint16_t*)cen, cprep, cnorm, C);
   hipLaunchKernelGGL((assign_kernel<0, KM_R>), dim3(cdiv(N, 128), H), dim3(256), 0, st,
                      (const uint16_t*)X, (const uint16_t*)cen, (const uint16_t*)cprep,
-                     (const float*)cnorm, lab, N, C, pin_begin, pin_label, 0);
+                     (const float*)cnorm, lab, N, C, pin_begin, pin_label, 0, guess);
   return t2t_check_launch("assign");
 }
 
@@ -596,14 +651,17 @@ static int kmm_impl(const void* QU, const void* KU, const void* V, int v_dtype,
   KmmWs w = kmm_layout(H, N, CQ, CK, ws);
   const int nores = N + 1;  // no pinned rows
   // query pass 1
-  KM_CHECK(launch_assign_km(QU, cq0, w.qlab1, H, N, CQ, nores, 0, w.cprep, w.cnorm, st));
+  // the label buffers' previous contents (the caller's labels of the last
+  // call, or anything) are warm-start guesses: pass 1 starts from qlab, pass 2
+  // from pass 1's labels, the key pass from klab
+  KM_CHECK(launch_assign_km(QU, cq0, w.qlab1, H, N, CQ, nores, 0, w.cprep, w.cnorm, qlab, st));
   KM_CHECK(run_sort(w.qlab1, w.counts1, w.cbase1, w.perm1, w.chist, H, N, CQ, st));
   hipLaunchKernelGGL(fixed_mean_kernel<0>, dim3(cdiv(CQ, 4), H), dim3(256), 0, st,
                      (const uint16_t*)QU, w.perm1, w.counts1, w.cbase1, (const uint16_t*)cq0,
                      w.cq1, N, CQ);
   T2T_LAUNCH_CHECK("qmean 1");
   // query pass 2
-  KM_CHECK(launch_assign_km(QU, w.cq1, qlab, H, N, CQ, nores, 0, w.cprep, w.cnorm, st));
+  KM_CHECK(launch_assign_km(QU, w.cq1, qlab, H, N, CQ, nores, 0, w.cprep, w.cnorm, w.qlab1, st));
   KM_CHECK(run_sort(qlab, qcounts, w.cbaseq, qperm, w.chist, H, N, CQ, st));
   hipLaunchKernelGGL(fixed_mean_kernel<0>, dim3(cdiv(CQ, 4), H), dim3(256), 0, st,
                      (const uint16_t*)QU, qperm, qcounts, w.cbaseq, (const uint16_t*)w.cq1,
@@ -611,7 +669,7 @@ static int kmm_impl(const void* QU, const void* KU, const void* V, int v_dtype,
   T2T_LAUNCH_CHECK("qmean 2");
   // key pass
   KM_CHECK(launch_assign_km(KU, ck0, klab, H, N, CK, pin_tail > 0 ? N - pin_tail : nores,
-                            CK - 1, w.cprep, w.cnorm, st));
+                            CK - 1, w.cprep, w.cnorm, klab, st));
   KM_CHECK(run_sort(klab, kcounts, w.cbasek, kperm, w.chist, H, N, CK, st));
   if (v_dtype == T2T_F16)
     launch_key_gather<F16T>(KU, V, kperm, kcounts, w.cbasek, ck0, ck2, V_sorted, w.vsum, w.cmax, H, N, CK,
@@ -762,15 +820,15 @@ extern "C" int t2t_fast_assign(const void* x, const void* c, int32_t* labels, in
   if (D == 32)
     hipLaunchKernelGGL((assign_kernel<1, 32>), g, dim3(256), 0, st, (const uint16_t*)x,
                        (const uint16_t*)c, (const uint16_t*)nullptr, (const float*)nullptr, labels, N, C,
-                       N + 1, 0, ibits);
+                       N + 1, 0, ibits, (const int32_t*)nullptr);
   else if (D == 64)
     hipLaunchKernelGGL((assign_kernel<1, 64>), g, dim3(256), 0, st, (const uint16_t*)x,
                        (const uint16_t*)c, (const uint16_t*)nullptr, (const float*)nullptr, labels, N, C,
-                       N + 1, 0, ibits);
+                       N + 1, 0, ibits, (const int32_t*)nullptr);
   else
     hipLaunchKernelGGL((assign_kernel<1, 128>), g, dim3(256), 0, st, (const uint16_t*)x,
                        (const uint16_t*)c, (const uint16_t*)nullptr, (const float*)nullptr, labels, N, C,
-                       N + 1, 0, ibits);
+                       N + 1, 0, ibits, (const int32_t*)nullptr);
   T2T_LAUNCH_CHECK("fast_assign");
   return T2T_OK;
 }

@@ -28,6 +28,12 @@
 // crossing high-byte bin to the lane's own slot: no conflicts, never read)
 #define SEL_HIST (256 + 64)
 
+// compiler-only ordering of LDS accesses (no wait): for wave-private LDS
+// data, whose accesses the wave's LDS queue performs in issue order
+__device__ inline void lds_order() { asm volatile("" ::: "memory"); }
+
+#define SEL_CAND 4  // window candidates per lane per round of LDS reads
+
 __device__ inline void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -252,9 +258,14 @@ __device__ inline int window_cross(const int (&key)[32], const uint16_t* krow, c
                                    int* hist, int ns, int lo, int* vstar, int* wgt, int* weq,
                                    int* ntie) {
   const int l = __lane_id();
+  // The histogram is private to the wave, and a wave's LDS instructions are
+  // performed in the order it issues them, so the clear, the adds and the
+  // reads below need no memory wait between them: the compiler barriers
+  // (lds_order) only keep the compiler from reordering them.
 #pragma unroll
   for (int i = 0; i < 2; ++i)
     *(u32x4*)(hist + 4 * (l + 64 * i)) = u32x4{0u, 0u, 0u, 0u};
+  lds_order();
   // the lane's keys at or above the window's base, as a mask: bit i = key[i]
   // >= lo, shifted in from bit 31 down (compare into VCC, then m + m + carry)
   uint32_t m = 0;
@@ -264,22 +275,33 @@ __device__ inline int window_cross(const int (&key)[32], const uint16_t* krow, c
         : "+v"(m)
         : "v"(key[i]), "v"(lo)
         : "vcc");
-  wave_sync();
   int aw = 0;  // the lane's weight above the window
-  while (__ballot(m != 0u) != 0ull) {  // wave-uniform
-    if (m != 0u) {
-      const int i = __builtin_ctz(m);
+  // candidates in rounds of SEL_CAND per lane: the round's key and size reads
+  // are issued together (one LDS latency per round, not per key); a lane with
+  // fewer candidates reads cluster 0 for the rest and adds nothing
+  do {
+    int c[SEL_CAND];
+    bool ok[SEL_CAND];
+#pragma unroll
+    for (int it = 0; it < SEL_CAND; ++it) {
+      ok[it] = m != 0u;
+      const int i = __builtin_ctz(m | 0x80000000u);
       m &= m - 1u;
-      const int c = 512 * (i >> 3) + 8 * l + (i & 7);  // cluster of key slot i
-      const int d = (int)(int16_t)krow[c] - lo;
-      const int sz = ssz[c];
-      if (d >= SEL_WIN)
-        aw += sz;
-      else
-        atomicAdd(&hist[d], (sz << 12) | 1);
+      c[it] = ok[it] ? 512 * (i >> 3) + 8 * l + (i & 7) : 0;  // cluster of key slot i
     }
-  }
-  wave_sync();
+    int d[SEL_CAND], sz[SEL_CAND];
+#pragma unroll
+    for (int it = 0; it < SEL_CAND; ++it) {
+      d[it] = (int)(int16_t)krow[c[it]] - lo;
+      sz[it] = ssz[c[it]];
+    }
+#pragma unroll
+    for (int it = 0; it < SEL_CAND; ++it) {
+      aw += ok[it] && d[it] >= SEL_WIN ? sz[it] : 0;
+      if (ok[it] && d[it] < SEL_WIN) atomicAdd(&hist[d[it]], (sz[it] << 12) | 1);
+    }
+  } while (__ballot(m != 0u) != 0ull);  // wave-uniform
+  lds_order();
   // lane l scans bins 511 - 8 l .. 504 - 8 l (descending keys)
   int raw[8];
   int s = 0;
@@ -291,7 +313,7 @@ __device__ inline int window_cross(const int (&key)[32], const uint16_t* krow, c
   const int above = wave_sum(aw);
   const int inc = wave_incl_scan(s);
   const int total = above + __builtin_amdgcn_readlane(inc, 63);
-  wave_sync();
+  lds_order();
   if (above >= ns) return 1;  // wave-uniform: the crossing is above the window
   if (total < ns) return -1;  // below it
   const int ex = inc - s + above;
@@ -540,13 +562,20 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
     __syncthreads();
     // every wave is past the previous batch: its counter can be reset
     if (threadIdx.x == 0) sNext[(b + 1) & 1] = 0;
-#pragma unroll 1
-    for (;;) {
+    // the next row is taken from the counter while the current one is
+    // selected, so the atomic's latency is hidden
+    auto grab = [&]() {
       int r = 0;
       if (l == 0) r = atomicAdd(&sNext[b & 1], 1);
-      r = __builtin_amdgcn_readfirstlane(r);
+      return r;
+    };
+    int rnext = grab();
+#pragma unroll 1
+    for (;;) {
+      const int r = __builtin_amdgcn_readfirstlane(rnext);
       const int j = j0 + r;
       if (r >= SF_ROWS || j >= lim) break;  // wave-uniform (rows only grow per wave)
+      rnext = grab();
       if (j >= tend) {      // wave-uniform: every lane takes part in the shuffles
         if (t >= 0) flush_union(acc, uh + (size_t)t * (SEL_NC / 32));
         acc = 0;

@@ -31,7 +31,7 @@
 
 // ---------------------------------------------------------------------------
 // plan layout (int32): k_off [H][2049] | kvlen [H][CQ] | ntask [H] |
-//                      tasks [H][maxT][4] = (cluster, sorted start, rows, 0)
+//                      tasks [H][maxT][4] = (cluster, sorted start, rows, cluster task rows)
 // ---------------------------------------------------------------------------
 static inline int plan_max_tasks(int N, int CQ) { return CQ + cdiv(N, TA_QT) + 1; }
 
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t* __restrict__ 
     if (lane == 0) kvlen[(size_t)h * CQ + t] = s;
   }
   __syncthreads();
-  // task list: cluster t splits into ceil(n / QT) balanced tasks
+  // task list: cluster t splits into ceil(n / QT) tasks of whole waves
   if (tid == 0) carry = 0;
   __syncthreads();
   __shared__ int qcarry;
@@ -126,15 +126,20 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t* __restrict__ 
     for (int i = 0; i < w; ++i) qex += wsum[i];
     const int tot_q = [&] { int s = 0; for (int i = 0; i < 16; ++i) s += wsum[i]; return s; }();
     if (t < CQ && nt > 0) {
-      const int base = n / nt, rem = n % nt;
+      // the cluster's ceil(n / 32) waves of 32 queries are dealt evenly over
+      // its tasks; only the last task holds a partial wave, so the tasks pad
+      // no more query rows than the cluster needs (an even split of the rows
+      // would pad every task's last wave)
+      const int nw = (n + 31) / 32;
+      const int base = nw / nt, rem = nw % nt;
       int s = qex;
       for (int i = 0; i < nt; ++i) {
-        const int rows = base + (i < rem ? 1 : 0);
+        const int rows = min(32 * (base + (i < rem ? 1 : 0)), qex + n - s);
         int32_t* tk = th + (size_t)(tex + i) * 4;
         tk[0] = t;
         tk[1] = s;
         tk[2] = rows;
-        tk[3] = 0;
+        tk[3] = 32 * (base + (rem > 0 ? 1 : 0));  // the cluster's largest task
         s += rows;
       }
     }
@@ -149,7 +154,9 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t* __restrict__ 
   if (tid == 0) ntask[h] = nT;
   __syncthreads();
   if (nT > PLAN_SORT_MAX || nT < 2) return;
-  // LPT order: descending rows x kv_len, ties by lower task index
+  // LPT order: descending (largest task rows of the cluster) x kv_len, ties
+  // by lower task index, so the tasks of one query cluster, which stream the
+  // same key/value union, stay next to each other and run on one XCD
   int P2 = 2;
   while (P2 < nT) P2 <<= 1;
   for (int i = tid; i < P2; i += 1024) {
@@ -157,7 +164,7 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int32_t* __restrict__ 
     if (i < nT) {
       const int32_t* tk = th + (size_t)i * 4;
       unsigned long long work =
-          (unsigned long long)tk[2] * (unsigned long long)kvlen[(size_t)h * CQ + tk[0]];
+          (unsigned long long)tk[3] * (unsigned long long)kvlen[(size_t)h * CQ + tk[0]];
       if (work > 0xFFFFFFFFull) work = 0xFFFFFFFFull;
       key = (work << 32) | (unsigned long long)(0x7FFFFFFF - i);
     }
