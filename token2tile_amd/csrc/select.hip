@@ -114,7 +114,40 @@ __device__ inline int find_cross(const int* hist, int base, int ns, int* above, 
   return __builtin_amdgcn_readlane(bin, src);
 }
 
-// Selection of one row.  keys/sz: the lane's 32 clusters (index 8 g + j).
+// the order keys of a pair of fp16 scores (score_key on each half): the sign
+// of each half spread over it (v_pk_ashrrev_i16), then x ^ (sign & 0x7FFF)
+// per half in one three-input bit operation
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t key_pair(uint32_t x) {
+  const uint32_t sm = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2, x) >> (s16x2){15, 15});
+  return x ^ (sm & 0x7FFF7FFFu);
+}
+
+// The lane's 32 order keys stay packed two to a dword as they sit in the
+// score row: slot i (cluster 512 (i / 8) + 8 lane + i % 8) is the low (i even)
+// or high (i odd) half of kp[i / 2].
+__device__ inline int key_at(const uint32_t (&kp)[16], int i) {
+  return (int)(int16_t)(uint16_t)((i & 1) ? kp[i >> 1] >> 16 : kp[i >> 1] & 0xffffu);
+}
+// bit i = (key i OP t), OP = ge / gt / eq: one compare per key on its
+// sign-extended half (SDWA) into VCC, then m + m + carry, from slot 31 down
+#define KEY_MASK_STEP(CMP, SEL)                                                        \
+  asm("v_cmp_" CMP "_i32_sdwa vcc, sext(%1), %2 src0_sel:" SEL " src1_sel:DWORD\n\t" \
+      "v_addc_co_u32 %0, vcc, %0, %0, vcc"                                            \
+      : "+v"(m)                                                                        \
+      : "v"(kp[i >> 1]), "v"(t)                                                        \
+      : "vcc")
+#define KEY_MASK_BODY(CMP)                                        \
+  uint32_t m = 0;                                                 \
+  _Pragma("unroll") for (int i = 31; i >= 0; --i) {               \
+    if (i & 1) KEY_MASK_STEP(CMP, "WORD_1"); else KEY_MASK_STEP(CMP, "WORD_0"); \
+  }                                                               \
+  return m;
+__device__ inline uint32_t keys_ge(const uint32_t (&kp)[16], int t) { KEY_MASK_BODY("ge") }
+__device__ inline uint32_t keys_gt(const uint32_t (&kp)[16], int t) { KEY_MASK_BODY("gt") }
+__device__ inline uint32_t keys_eq(const uint32_t (&kp)[16], int t) { KEY_MASK_BODY("eq") }
+
+// Selection of one row.  kp/sz: the lane's 32 clusters (index 8 g + j).
 // Returns the lane's 32 selection bits; *rowcnt = selected keys (all lanes);
 // *vstar_out = the row's crossing key.
 //
@@ -126,11 +159,11 @@ __device__ inline int find_cross(const int* hist, int base, int ns, int* above, 
 // the clusters with keys >= lo hold >= ns keys: the crossing key is then >= lo
 // and every key at or above it is counted.  Otherwise the row is redone
 // without the bound.
-__device__ inline uint32_t select_bits(const int (&key)[32], const int (&sz)[32], int ns, int vstar,
-                                       int wgt, int weq, int ntie, int* rowcnt);
+__device__ inline uint32_t select_bits(const uint32_t (&kp)[16], const int (&sz)[32], int ns,
+                                       int vstar, int wgt, int weq, int ntie, int* rowcnt);
 #define SEL_NO_BOUND (-65536)
 #define SEL_BOUND_MARGIN 1024  // one binade of fp16 keys
-__device__ inline void radix_cross(const int (&key)[32], const int (&sz)[32], int* hist, int ns,
+__device__ inline void radix_cross(const uint32_t (&kp)[16], const int (&sz)[32], int* hist, int ns,
                                    int lo, int* vstar_out, int* wgt_out, int* weq_out,
                                    int* ntie_out) {
   const int l = __lane_id();
@@ -141,8 +174,10 @@ __device__ inline void radix_cross(const int (&key)[32], const int (&sz)[32], in
     for (int i = 0; i < 4; ++i) hist[4 * l + i] = 0;
     wave_sync();
 #pragma unroll
-    for (int i = 0; i < 32; ++i)  // empty clusters add 0
-      atomicAdd(&hist[key[i] >= lo ? (key[i] >> 8) + 128 : 256 + l], sz[i]);
+    for (int i = 0; i < 32; ++i) {  // empty clusters add 0
+      const int key = key_at(kp, i);
+      atomicAdd(&hist[key >= lo ? (key >> 8) + 128 : 256 + l], sz[i]);
+    }
     wave_sync();
     hb = find_cross(hist, 0, ns, &above1, &inbin1, &tot1);
     wave_sync();
@@ -155,9 +190,11 @@ __device__ inline void radix_cross(const int (&key)[32], const int (&sz)[32], in
   wave_sync();
   const int hsel = hb - 128;
 #pragma unroll
-  for (int i = 0; i < 32; ++i)
-    atomicAdd(&hist[(key[i] >> 8) == hsel && key[i] >= lo ? (key[i] & 255) : 256 + l],
+  for (int i = 0; i < 32; ++i) {
+    const int key = key_at(kp, i);
+    atomicAdd(&hist[(key >> 8) == hsel && key >= lo ? (key & 255) : 256 + l],
               (sz[i] << 12) | 1);  // weight and key count (weights < 2^19, counts < 2^12)
+  }
   wave_sync();
   int wgt, weq, tot2, ntie;
   const int lb = find_cross<true>(hist, above1, ns, &wgt, &weq, &tot2, &ntie);
@@ -167,32 +204,23 @@ __device__ inline void radix_cross(const int (&key)[32], const int (&sz)[32], in
   *weq_out = weq;
   *ntie_out = ntie;
 }
-__device__ inline uint32_t select_row(const int (&key)[32], const int (&sz)[32], int* hist, int ns,
+__device__ inline uint32_t select_row(const uint32_t (&kp)[16], const int (&sz)[32], int* hist, int ns,
                                       int lo, int* rowcnt, int* vstar_out) {
   int wgt, weq, ntie;
-  radix_cross(key, sz, hist, ns, lo, vstar_out, &wgt, &weq, &ntie);
-  return select_bits(key, sz, ns, *vstar_out, wgt, weq, ntie, rowcnt);
+  radix_cross(kp, sz, hist, ns, lo, vstar_out, &wgt, &weq, &ntie);
+  return select_bits(kp, sz, ns, *vstar_out, wgt, weq, ntie, rowcnt);
 }
 
 // The lane's 32 selection bits given the crossing key vstar of the row, the
 // weight wgt of all keys above it, the weight weq and number ntie of the
 // clusters holding vstar; *rowcnt = selected keys.  Ties at the threshold
 // (ntie > 1) are taken in ascending cluster order.
-__device__ inline uint32_t select_bits(const int (&key)[32], const int (&sz)[32], int ns, int vstar,
-                                       int wgt, int weq, int ntie, int* rowcnt) {
+__device__ inline uint32_t select_bits(const uint32_t (&kp)[16], const int (&sz)[32], int ns,
+                                       int vstar, int wgt, int weq, int ntie, int* rowcnt) {
   const int l = __lane_id();
-  uint32_t bits = 0;
   if (ntie == 1) {
-    // bit i = key[i] >= vstar, shifted in from bit 31 down: compare into VCC,
-    // then bits = bits + bits + carry (two instructions per key)
-#pragma unroll
-    for (int i = 31; i >= 0; --i)
-      asm("v_cmp_ge_i32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
-          : "+v"(bits)
-          : "v"(key[i]), "v"(vstar)
-          : "vcc");
     *rowcnt = wgt + weq;
-    return bits;
+    return keys_ge(kp, vstar);
   }
   // ---- several clusters on the key vstar: all keys above it are taken
   //      (weight wgt < ns), then the tied clusters in ascending cluster order
@@ -200,18 +228,7 @@ __device__ inline uint32_t select_bits(const int (&key)[32], const int (&sz)[32]
   //      cluster where it does is istar, and every tied cluster up to it is
   //      taken, empty ones included
   const int R = ns - wgt;  // >= 1
-  uint32_t gt = 0, tie = 0;
-#pragma unroll
-  for (int i = 31; i >= 0; --i) {
-    asm("v_cmp_gt_i32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
-        : "+v"(gt)
-        : "v"(key[i]), "v"(vstar)
-        : "vcc");
-    asm("v_cmp_eq_i32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
-        : "+v"(tie)
-        : "v"(key[i]), "v"(vstar)
-        : "vcc");
-  }
+  const uint32_t gt = keys_gt(kp, vstar), tie = keys_eq(kp, vstar);
   int cum = 0, istar = -1;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -254,7 +271,7 @@ __device__ inline uint32_t select_bits(const int (&key)[32], const int (&sz)[32]
 // above the window) or -1 (below it).
 #define SEL_WIN 512
 #define SEL_WHIST SEL_WIN  // window bins (the radix fallback uses the first 320)
-__device__ inline int window_cross(const int (&key)[32], const uint16_t* krow, const int* ssz,
+__device__ inline int window_cross(const uint32_t (&kp)[16], const uint16_t* krow, const int* ssz,
                                    int* hist, int ns, int lo, int* vstar, int* wgt, int* weq,
                                    int* ntie) {
   const int l = __lane_id();
@@ -266,15 +283,8 @@ __device__ inline int window_cross(const int (&key)[32], const uint16_t* krow, c
   for (int i = 0; i < 2; ++i)
     *(u32x4*)(hist + 4 * (l + 64 * i)) = u32x4{0u, 0u, 0u, 0u};
   lds_order();
-  // the lane's keys at or above the window's base, as a mask: bit i = key[i]
-  // >= lo, shifted in from bit 31 down (compare into VCC, then m + m + carry)
-  uint32_t m = 0;
-#pragma unroll
-  for (int i = 31; i >= 0; --i)
-    asm("v_cmp_ge_i32 vcc, %1, %2\n\tv_addc_co_u32 %0, vcc, %0, %0, vcc"
-        : "+v"(m)
-        : "v"(key[i]), "v"(lo)
-        : "vcc");
+  // the lane's keys at or above the window's base, as a mask
+  uint32_t m = keys_ge(kp, lo);
   int aw = 0;  // the lane's weight above the window
   // candidates in rounds of SEL_CAND per lane: the round's key and size reads
   // are issued together (one LDS latency per round, not per key); a lane with
@@ -416,19 +426,16 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
       } while (j >= tend);
     }
     const int orig = qp[j];
-    int key[32];
+    uint32_t kp[16];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const u32x4 v = __builtin_nontemporal_load(
           (const u32x4*)(glh + (size_t)orig * SEL_NC + 512 * g + 8 * l));
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        key[8 * g + 2 * q] = score_key((uint16_t)(v[q] & 0xffff));
-        key[8 * g + 2 * q + 1] = score_key((uint16_t)(v[q] >> 16));
-      }
+      for (int q = 0; q < 4; ++q) kp[4 * g + q] = key_pair(v[q]);
     }
     int rc;
-    acc |= select_row(key, sz, hist, ns, klo, &rc, &vstar);
+    acc |= select_row(kp, sz, hist, ns, klo, &rc, &vstar);
     klo = vstar - SEL_BOUND_MARGIN;
     if (l == 0) rowcnt[(size_t)h * N + orig] = rc;
   }
@@ -451,15 +458,6 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
 // being selected.  The centroid fragments are reloaded (from L2) per batch,
 // which keeps their 64 registers free during the selection.
 // ---------------------------------------------------------------------------
-// the order keys of a pair of fp16 scores (score_key on each half): the sign
-// of each half spread over it (v_pk_ashrrev_i16), then x ^ (sign & 0x7FFF)
-// per half in one three-input bit operation
-typedef short s16x2 __attribute__((ext_vector_type(2)));
-__device__ inline uint32_t key_pair(uint32_t x) {
-  const uint32_t sm = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2, x) >> (s16x2){15, 15});
-  return x ^ (sm & 0x7FFF7FFFu);
-}
-
 #define SF_WAVES 8
 #define SF_ROWS 32
 #define SF_BATCHES 16
@@ -590,16 +588,13 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
         while (t < CQ - 1 && offh[t + 1] <= j) ++t;  // next non-empty cluster
         tend = offh[t + 1];
       }
-      int key[32];
+      uint32_t kp[16];
       const uint16_t* kr = sKey + r * SF_PITCH;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const u32x4 v = *(const u32x4*)(kr + 512 * g + 8 * l);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          key[8 * g + 2 * q] = (int)(int16_t)(uint16_t)(v[q] & 0xffffu);
-          key[8 * g + 2 * q + 1] = (int)(int16_t)(uint16_t)(v[q] >> 16);
-        }
+        for (int q = 0; q < 4; ++q) kp[4 * g + q] = v[q];
       }
       int rc;
       // the window around the previous row's crossing first; the full search
@@ -608,16 +603,16 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
       int where = 0;
       if (klo != SEL_NO_BOUND) {
         const int lo = vstar - SEL_WIN / 2;
-        where = window_cross(key, kr, sSz, hist, ns, lo, &vs, &wgt, &weq, &ntie);
+        where = window_cross(kp, kr, sSz, hist, ns, lo, &vs, &wgt, &weq, &ntie);
         if (where > 0)  // the crossing is above the window: the window above it
-          where = window_cross(key, kr, sSz, hist, ns, lo + SEL_WIN, &vs, &wgt, &weq, &ntie);
+          where = window_cross(kp, kr, sSz, hist, ns, lo + SEL_WIN, &vs, &wgt, &weq, &ntie);
         else if (where < 0)  // below it: the window below
-          where = window_cross(key, kr, sSz, hist, ns, lo - SEL_WIN, &vs, &wgt, &weq, &ntie);
+          where = window_cross(kp, kr, sSz, hist, ns, lo - SEL_WIN, &vs, &wgt, &weq, &ntie);
       }
       if (where != 0 || klo == SEL_NO_BOUND)
-        radix_cross(key, sz, hist, ns, klo, &vs, &wgt, &weq, &ntie);
+        radix_cross(kp, sz, hist, ns, klo, &vs, &wgt, &weq, &ntie);
       vstar = vs;
-      acc |= select_bits(key, sz, ns, vstar, wgt, weq, ntie, &rc);
+      acc |= select_bits(kp, sz, ns, vstar, wgt, weq, ntie, &rc);
       klo = vstar - SEL_BOUND_MARGIN;
       if (l == 0) rowcnt[(size_t)h * N + qp[j]] = rc;
     }
