@@ -6,51 +6,71 @@
 // four consecutive output features per accumulator group.
 #include "t2t_common.h"
 
+// work-groups of one projection launch, over all heads (32 per CU)
+#define T2T_PROJ_WGS 8192
+
 // ---------------------------------------------------------------------------
 // S1: out[n, 0:32] = fp16(x[n, 0:D] @ U[0:D, 0:32]), fp32 accumulation
 // ---------------------------------------------------------------------------
+// Persistent: up to 8192 work-groups walk the head's 32-row blocks; U is
+// staged once per work-group through LDS, and each wave keeps the next
+// block's x loads in flight while it multiplies and stores the current one.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void project_kernel(const uint16_t* __restrict__ x,
                                                       const uint16_t* __restrict__ U,
                                                       uint16_t* __restrict__ out, int N,
                                                       long long sxh, long long sxn) {
   constexpr int KS = D / 16;
+  __shared__ uint16_t sU[D * 32];
   const int h = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int jl = lane & 31, hh = lane >> 5;
   const uint16_t* Uh = U + (size_t)h * D * 32;
+  for (int i = threadIdx.x; i < D * 32 / 8; i += 256) ((u32x4*)sU)[i] = ((const u32x4*)Uh)[i];
+  __syncthreads();
   // A operand = U^T: lane supplies U[16 s + 8 hh + t][jl]
   u32x4 ua[KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    uint16_t v[8];
+  for (int s = 0; s < KS; ++s)
 #pragma unroll
-    for (int t = 0; t < 8; ++t) v[t] = Uh[(size_t)(16 * s + 8 * hh + t) * 32 + jl];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) ua[s][t] = (uint32_t)v[2 * t] | ((uint32_t)v[2 * t + 1] << 16);
-  }
+    for (int t = 0; t < 4; ++t)
+      ua[s][t] = (uint32_t)sU[(16 * s + 8 * hh + 2 * t) * 32 + jl] |
+                 ((uint32_t)sU[(16 * s + 8 * hh + 2 * t + 1) * 32 + jl] << 16);
   // x row n of head h at x + h sxh + n sxn (elements): [H, N, D] contiguous
   // or a strided view such as the token-major [N, H, D]
   const uint16_t* xh = x + (size_t)h * sxh;
   uint16_t* oh = out + (size_t)h * N * 32;
-  for (int r0 = (blockIdx.x * 4 + wave) * 32; r0 < N; r0 += gridDim.x * 4 * 32) {
+  const int step = gridDim.x * 4 * 32;
+  auto load = [&](int r0, u32x4 (&b)[KS]) {
     const int row = r0 + jl;
-    const bool ok = row < N;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) b[s] = u32x4{0u, 0u, 0u, 0u};
+    if (row < N)
+#pragma unroll
+      for (int s = 0; s < KS; ++s) b[s] = *(const u32x4*)(xh + (size_t)row * sxn + 16 * s + 8 * hh);
+  };
+  int r0 = (blockIdx.x * 4 + wave) * 32;
+  u32x4 bn[KS];
+  if (r0 < N) load(r0, bn);
+  for (; r0 < N; r0 += step) {
+    u32x4 b[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) b[s] = bn[s];
+    if (r0 + step < N) load(r0 + step, bn);
+    const int row = r0 + jl;
     f32x16 acc = zero16();
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      u32x4 b = {0u, 0u, 0u, 0u};
-      if (ok) b = *(const u32x4*)(xh + (size_t)row * sxn + 16 * s + 8 * hh);
       if constexpr (T::code == T2T_BF16) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const uint32_t w = b[t];
-          b[t] = (uint32_t)bf2h((uint16_t)(w & 0xffff)) | ((uint32_t)bf2h((uint16_t)(w >> 16)) << 16);
+          const uint32_t w = b[s][t];
+          b[s][t] = (uint32_t)bf2h((uint16_t)(w & 0xffff)) | ((uint32_t)bf2h((uint16_t)(w >> 16)) << 16);
         }
       }
-      acc = Mfma<F16T>::run(ua[s], b, acc);
+      acc = Mfma<F16T>::run(ua[s], b[s], acc);
     }
-    if (ok) {
+    if (row < N) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         u32x2 o;
@@ -66,7 +86,8 @@ template <typename T>
 static int launch_project(const void* x, const void* U, void* out, int H, int N, int D,
                           long long sxh, long long sxn, hipStream_t st) {
   int gx = cdiv(N, 128);
-  if (gx > 1024) gx = 1024;
+  const int cap = (T2T_PROJ_WGS + H - 1) / H;
+  if (gx > cap) gx = cap;
   dim3 grid(gx, H);
   switch (D) {
     case 128:
