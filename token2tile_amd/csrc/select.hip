@@ -126,6 +126,8 @@ __device__ inline uint32_t key_pair(uint32_t x) {
 // The lane's 32 order keys stay packed two to a dword as they sit in the
 // score row: slot i (cluster 512 (i / 8) + 8 lane + i % 8) is the low (i even)
 // or high (i odd) half of kp[i / 2].
+// cluster of slot i of lane l
+__device__ inline int slot_cluster(int i, int l) { return 512 * (i >> 3) + 8 * l + (i & 7); }
 __device__ inline int key_at(const uint32_t (&kp)[16], int i) {
   return (int)(int16_t)(uint16_t)((i & 1) ? kp[i >> 1] >> 16 : kp[i >> 1] & 0xffffu);
 }
@@ -147,7 +149,8 @@ __device__ inline uint32_t keys_ge(const uint32_t (&kp)[16], int t) { KEY_MASK_B
 __device__ inline uint32_t keys_gt(const uint32_t (&kp)[16], int t) { KEY_MASK_BODY("gt") }
 __device__ inline uint32_t keys_eq(const uint32_t (&kp)[16], int t) { KEY_MASK_BODY("eq") }
 
-// Selection of one row.  kp/sz: the lane's 32 clusters (index 8 g + j).
+// Selection of one row.  kp: the lane's 32 clusters (index 8 g + j); ssz: the
+// head's cluster sizes (LDS).
 // Returns the lane's 32 selection bits; *rowcnt = selected keys (all lanes);
 // *vstar_out = the row's crossing key.
 //
@@ -159,11 +162,11 @@ __device__ inline uint32_t keys_eq(const uint32_t (&kp)[16], int t) { KEY_MASK_B
 // the clusters with keys >= lo hold >= ns keys: the crossing key is then >= lo
 // and every key at or above it is counted.  Otherwise the row is redone
 // without the bound.
-__device__ inline uint32_t select_bits(const uint32_t (&kp)[16], const int (&sz)[32], int ns,
-                                       int vstar, int wgt, int weq, int ntie, int* rowcnt);
+__device__ inline uint32_t select_bits(const uint32_t (&kp)[16], const int* ssz, int ns, int vstar,
+                                       int wgt, int weq, int ntie, int* rowcnt);
 #define SEL_NO_BOUND (-65536)
 #define SEL_BOUND_MARGIN 1024  // one binade of fp16 keys
-__device__ inline void radix_cross(const uint32_t (&kp)[16], const int (&sz)[32], int* hist, int ns,
+__device__ inline void radix_cross(const uint32_t (&kp)[16], const int* ssz, int* hist, int ns,
                                    int lo, int* vstar_out, int* wgt_out, int* weq_out,
                                    int* ntie_out) {
   const int l = __lane_id();
@@ -176,7 +179,7 @@ __device__ inline void radix_cross(const uint32_t (&kp)[16], const int (&sz)[32]
 #pragma unroll
     for (int i = 0; i < 32; ++i) {  // empty clusters add 0
       const int key = key_at(kp, i);
-      atomicAdd(&hist[key >= lo ? (key >> 8) + 128 : 256 + l], sz[i]);
+      atomicAdd(&hist[key >= lo ? (key >> 8) + 128 : 256 + l], ssz[slot_cluster(i, l)]);
     }
     wave_sync();
     hb = find_cross(hist, 0, ns, &above1, &inbin1, &tot1);
@@ -193,7 +196,7 @@ __device__ inline void radix_cross(const uint32_t (&kp)[16], const int (&sz)[32]
   for (int i = 0; i < 32; ++i) {
     const int key = key_at(kp, i);
     atomicAdd(&hist[(key >> 8) == hsel && key >= lo ? (key & 255) : 256 + l],
-              (sz[i] << 12) | 1);  // weight and key count (weights < 2^19, counts < 2^12)
+              (ssz[slot_cluster(i, l)] << 12) | 1);  // weight and key count (weights < 2^19, counts < 2^12)
   }
   wave_sync();
   int wgt, weq, tot2, ntie;
@@ -204,19 +207,19 @@ __device__ inline void radix_cross(const uint32_t (&kp)[16], const int (&sz)[32]
   *weq_out = weq;
   *ntie_out = ntie;
 }
-__device__ inline uint32_t select_row(const uint32_t (&kp)[16], const int (&sz)[32], int* hist, int ns,
+__device__ inline uint32_t select_row(const uint32_t (&kp)[16], const int* ssz, int* hist, int ns,
                                       int lo, int* rowcnt, int* vstar_out) {
   int wgt, weq, ntie;
-  radix_cross(kp, sz, hist, ns, lo, vstar_out, &wgt, &weq, &ntie);
-  return select_bits(kp, sz, ns, *vstar_out, wgt, weq, ntie, rowcnt);
+  radix_cross(kp, ssz, hist, ns, lo, vstar_out, &wgt, &weq, &ntie);
+  return select_bits(kp, ssz, ns, *vstar_out, wgt, weq, ntie, rowcnt);
 }
 
 // The lane's 32 selection bits given the crossing key vstar of the row, the
 // weight wgt of all keys above it, the weight weq and number ntie of the
 // clusters holding vstar; *rowcnt = selected keys.  Ties at the threshold
 // (ntie > 1) are taken in ascending cluster order.
-__device__ inline uint32_t select_bits(const uint32_t (&kp)[16], const int (&sz)[32], int ns,
-                                       int vstar, int wgt, int weq, int ntie, int* rowcnt) {
+__device__ inline uint32_t select_bits(const uint32_t (&kp)[16], const int* ssz, int ns, int vstar,
+                                       int wgt, int weq, int ntie, int* rowcnt) {
   const int l = __lane_id();
   if (ntie == 1) {
     *rowcnt = wgt + weq;
@@ -240,7 +243,7 @@ __device__ inline uint32_t select_bits(const uint32_t (&kp)[16], const int (&sz)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         if (istar < 0 && ((byte >> j) & 1u)) {
-          cum += __builtin_amdgcn_readlane(sz[8 * g + j], L);
+          cum += ssz[512 * g + 8 * L + j];
           if (cum >= R) istar = 512 * g + 8 * L + j;
         }
       }
@@ -376,9 +379,12 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
     const int32_t* __restrict__ ns_dev, int32_t* __restrict__ unip, int32_t* __restrict__ rowcnt,
     int N, int CQ) {
   __shared__ int hist_all[SEL_WAVES][SEL_HIST];
+  __shared__ int sSz[SEL_NC];  // the head's key-cluster sizes
   const int h = blockIdx.y;
   const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
   int* hist = hist_all[wv];
+  for (int c = threadIdx.x; c < SEL_NC; c += SEL_WAVES * 64) sSz[c] = kcounts[(size_t)h * SEL_NC + c];
+  __syncthreads();
   const int32_t* offh = off + (size_t)h * (CQ + 1);
   const int total = offh[CQ];
   int j0 = (blockIdx.x * SEL_WAVES + wv) * SEL_ROWS_PER_WAVE;
@@ -386,17 +392,13 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
   if (j1 > total) j1 = total;
   if (j1 > N) j1 = N;  // qcounts summing past N is invalid input; never read past N
   if (j0 >= j1) return;
-  // cluster sizes of the lane's 32 clusters, and the key total
-  int sz[32];
+  // the key total
   int ktot = 0;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int32_t* p = kcounts + (size_t)h * SEL_NC + 512 * g + 8 * l;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      sz[8 * g + j] = p[j];
-      ktot += p[j];
-    }
+    for (int j = 0; j < 8; ++j) ktot += p[j];
   }
   ktot = wave_sum(ktot);
   int ns = *ns_dev;
@@ -435,7 +437,7 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
       for (int q = 0; q < 4; ++q) kp[4 * g + q] = key_pair(v[q]);
     }
     int rc;
-    acc |= select_row(kp, sz, hist, ns, klo, &rc, &vstar);
+    acc |= select_row(kp, sSz, hist, ns, klo, &rc, &vstar);
     klo = vstar - SEL_BOUND_MARGIN;
     if (l == 0) rowcnt[(size_t)h * N + orig] = rc;
   }
@@ -455,8 +457,7 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
 // passes only when both miss (a few rows in 10^4 at 720p).  A work-group
 // walks 16 batches (512 rows): the cluster sizes it loads once are amortised
 // over them, and the next batch's query rows load while the current batch is
-// being selected.  The centroid fragments are reloaded (from L2) per batch,
-// which keeps their 64 registers free during the selection.
+// being selected.  The wave's centroid fragments are loaded once and held.
 // ---------------------------------------------------------------------------
 #define SF_WAVES 8
 #define SF_ROWS 32
@@ -484,26 +485,20 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
   if (lim > N) lim = N;  // qcounts summing past N is invalid input; never read past N
   const int base = blockIdx.x * SF_ROWS * SF_BATCHES;
   if (base >= lim) return;
-  // cluster sizes of the lane's 32 selection clusters, and the key total
-  int sz[32];
+  // the key total
   int ktot = 0;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int32_t* p = kcounts + (size_t)h * SEL_NC + 512 * g + 8 * l;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      sz[8 * g + j] = p[j];
-      ktot += p[j];
-    }
+    for (int j = 0; j < 8; ++j) ktot += p[j];
   }
   ktot = wave_sum(ktot);
   int ns = *ns_dev;
   ns = ns < 1 ? 1 : ns;
   ns = ns > ktot ? ktot : ns;
   // centroid fragments of the wave's 256 centroids (the A operands of
-  // score_kernel: row 32 cb + jl, dims 8 hh .. and 16 + 8 hh ..), loaded
-  // (from L2) for each batch's scoring, so that their 64 registers are free
-  // during the selection
+  // score_kernel: row 32 cb + jl, dims 8 hh .. and 16 + 8 hh ..)
   const uint16_t* ch = cks + ((size_t)h * SEL_NC + 256 * wv + jl) * 32 + 8 * hh;
   const int32_t* qp = qperm + (size_t)h * N;
   const uint16_t* qh = QU + (size_t)h * N * 32;
@@ -525,6 +520,13 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
   };
   u32x4 b0, b1;
   load_rows(base, b0, b1);
+  // the wave's centroid fragments, held for all batches
+  u32x4 ca0[8], ca1[8];
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb) {
+    ca0[cb] = *(const u32x4*)(ch + cb * 32 * 32);
+    ca1[cb] = *(const u32x4*)(ch + cb * 32 * 32 + 16);
+  }
   if (threadIdx.x < 2) sNext[threadIdx.x] = 0;
   for (int c = threadIdx.x; c < SEL_NC; c += SF_WAVES * 64) sSz[c] = kcounts[(size_t)h * SEL_NC + c];
   for (int b = 0; b < SF_BATCHES; ++b) {
@@ -532,12 +534,6 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
     if (j0 >= lim) break;
     {  // scores of rows j0 .. j0 + 31 against the wave's centroids -> keys in LDS
       uint16_t* krow = sKey + jl * SF_PITCH + 256 * wv + 4 * hh;
-      u32x4 ca0[8], ca1[8];
-#pragma unroll
-      for (int cb = 0; cb < 8; ++cb) {
-        ca0[cb] = *(const u32x4*)(ch + cb * 32 * 32);
-        ca1[cb] = *(const u32x4*)(ch + cb * 32 * 32 + 16);
-      }
 #pragma unroll
       for (int cb = 0; cb < 8; ++cb) {
         f32x16 sc = zero16();
@@ -610,9 +606,9 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
           where = window_cross(kp, kr, sSz, hist, ns, lo - SEL_WIN, &vs, &wgt, &weq, &ntie);
       }
       if (where != 0 || klo == SEL_NO_BOUND)
-        radix_cross(kp, sz, hist, ns, klo, &vs, &wgt, &weq, &ntie);
+        radix_cross(kp, sSz, hist, ns, klo, &vs, &wgt, &weq, &ntie);
       vstar = vs;
-      acc |= select_bits(kp, sz, ns, vstar, wgt, weq, ntie, &rc);
+      acc |= select_bits(kp, sSz, ns, vstar, wgt, weq, ntie, &rc);
       klo = vstar - SEL_BOUND_MARGIN;
       if (l == 0) rowcnt[(size_t)h * N + qp[j]] = rc;
     }
