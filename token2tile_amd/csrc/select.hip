@@ -32,7 +32,8 @@
 // data, whose accesses the wave's LDS queue performs in issue order
 __device__ inline void lds_order() { asm volatile("" ::: "memory"); }
 
-#define SEL_CAND 4  // window candidates per lane per round of LDS reads
+#define SEL_CAND1 4  // window candidates per lane in the first round of LDS reads
+#define SEL_CAND 4   // ... and in each further round
 
 __device__ inline void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -276,7 +277,7 @@ __device__ inline uint32_t select_bits(const uint32_t (&kp)[16], const int* ssz,
 #define SEL_WHIST SEL_WIN  // window bins (the radix fallback uses the first 320)
 __device__ inline int window_cross(const uint32_t (&kp)[16], const uint16_t* krow, const int* ssz,
                                    int* hist, int ns, int lo, int* vstar, int* wgt, int* weq,
-                                   int* ntie) {
+                                   int* ntie, uint32_t* bits, int* bits_ok) {
   const int l = __lane_id();
   // The histogram is private to the wave, and a wave's LDS instructions are
   // performed in the order it issues them, so the clear, the adds and the
@@ -289,10 +290,35 @@ __device__ inline int window_cross(const uint32_t (&kp)[16], const uint16_t* kro
   // the lane's keys at or above the window's base, as a mask
   uint32_t m = keys_ge(kp, lo);
   int aw = 0;  // the lane's weight above the window
-  // candidates in rounds of SEL_CAND per lane: the round's key and size reads
-  // are issued together (one LDS latency per round, not per key); a lane with
-  // fewer candidates reads cluster 0 for the rest and adds nothing
-  do {
+  // candidates in rounds per lane: a round's key and size reads are issued
+  // together (one LDS latency per round, not per key); a lane with fewer
+  // candidates reads cluster 0 for the rest and adds nothing.  The first
+  // round takes SEL_CAND1 and keeps their slots and keys, which give the
+  // selection bits directly when it was the only round
+  int slot1[SEL_CAND1], d1[SEL_CAND1];
+  bool ok1[SEL_CAND1];
+  {
+    int c[SEL_CAND1], sz[SEL_CAND1];
+#pragma unroll
+    for (int it = 0; it < SEL_CAND1; ++it) {
+      ok1[it] = m != 0u;
+      slot1[it] = __builtin_ctz(m | 0x80000000u);
+      m &= m - 1u;
+      c[it] = ok1[it] ? slot_cluster(slot1[it], l) : 0;
+    }
+#pragma unroll
+    for (int it = 0; it < SEL_CAND1; ++it) {
+      d1[it] = (int)(int16_t)krow[c[it]] - lo;
+      sz[it] = ssz[c[it]];
+    }
+#pragma unroll
+    for (int it = 0; it < SEL_CAND1; ++it) {
+      aw += ok1[it] && d1[it] >= SEL_WIN ? sz[it] : 0;
+      if (ok1[it] && d1[it] < SEL_WIN) atomicAdd(&hist[d1[it]], (sz[it] << 12) | 1);
+    }
+  }
+  const bool one_round = __ballot(m != 0u) == 0ull;  // wave-uniform
+  while (__ballot(m != 0u) != 0ull) {  // wave-uniform
     int c[SEL_CAND];
     bool ok[SEL_CAND];
 #pragma unroll
@@ -300,7 +326,7 @@ __device__ inline int window_cross(const uint32_t (&kp)[16], const uint16_t* kro
       ok[it] = m != 0u;
       const int i = __builtin_ctz(m | 0x80000000u);
       m &= m - 1u;
-      c[it] = ok[it] ? 512 * (i >> 3) + 8 * l + (i & 7) : 0;  // cluster of key slot i
+      c[it] = ok[it] ? slot_cluster(i, l) : 0;
     }
     int d[SEL_CAND], sz[SEL_CAND];
 #pragma unroll
@@ -313,7 +339,7 @@ __device__ inline int window_cross(const uint32_t (&kp)[16], const uint16_t* kro
       aw += ok[it] && d[it] >= SEL_WIN ? sz[it] : 0;
       if (ok[it] && d[it] < SEL_WIN) atomicAdd(&hist[d[it]], (sz[it] << 12) | 1);
     }
-  } while (__ballot(m != 0u) != 0ull);  // wave-uniform
+  }
   lds_order();
   // lane l scans bins 511 - 8 l .. 504 - 8 l (descending keys)
   int raw[8];
@@ -354,6 +380,17 @@ __device__ inline int window_cross(const uint32_t (&kp)[16], const uint16_t* kro
   raw_b = __builtin_amdgcn_readlane(raw_b, src);
   *weq = raw_b >> 12;
   *ntie = raw_b & 0xfff;
+  // one cluster at the crossing key: the selection is every key at or above
+  // it, all of them candidates (keys >= lo); from the first round's records
+  // when it held them all
+  *bits_ok = one_round && *ntie == 1;
+  if (*bits_ok) {
+    const int t = *vstar - lo;
+    uint32_t b = 0;
+#pragma unroll
+    for (int it = 0; it < SEL_CAND1; ++it) b |= ok1[it] && d1[it] >= t ? 1u << slot1[it] : 0u;
+    *bits = b;
+  }
   return 0;
 }
 
@@ -596,19 +633,29 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
       // the window around the previous row's crossing first; the full search
       // when the crossing lies outside it (or for the wave's first row)
       int vs, wgt, weq, ntie;
-      int where = 0;
+      int where = 0, bits_ok = 0;
+      uint32_t bits = 0;
       if (klo != SEL_NO_BOUND) {
         const int lo = vstar - SEL_WIN / 2;
-        where = window_cross(kp, kr, sSz, hist, ns, lo, &vs, &wgt, &weq, &ntie);
+        where = window_cross(kp, kr, sSz, hist, ns, lo, &vs, &wgt, &weq, &ntie, &bits, &bits_ok);
         if (where > 0)  // the crossing is above the window: the window above it
-          where = window_cross(kp, kr, sSz, hist, ns, lo + SEL_WIN, &vs, &wgt, &weq, &ntie);
+          where = window_cross(kp, kr, sSz, hist, ns, lo + SEL_WIN, &vs, &wgt, &weq, &ntie, &bits,
+                               &bits_ok);
         else if (where < 0)  // below it: the window below
-          where = window_cross(kp, kr, sSz, hist, ns, lo - SEL_WIN, &vs, &wgt, &weq, &ntie);
+          where = window_cross(kp, kr, sSz, hist, ns, lo - SEL_WIN, &vs, &wgt, &weq, &ntie, &bits,
+                               &bits_ok);
       }
-      if (where != 0 || klo == SEL_NO_BOUND)
+      if (where != 0 || klo == SEL_NO_BOUND) {
         radix_cross(kp, sSz, hist, ns, klo, &vs, &wgt, &weq, &ntie);
+        bits_ok = 0;
+      }
       vstar = vs;
-      acc |= select_bits(kp, sSz, ns, vstar, wgt, weq, ntie, &rc);
+      if (bits_ok) {  // wave-uniform
+        rc = wgt + weq;
+        acc |= bits;
+      } else {
+        acc |= select_bits(kp, sSz, ns, vstar, wgt, weq, ntie, &rc);
+      }
       klo = vstar - SEL_BOUND_MARGIN;
       if (l == 0) rowcnt[(size_t)h * N + qp[j]] = rc;
     }
