@@ -5,6 +5,7 @@
 // MFMA row axis, tokens on the column axis) so that a lane owns one token and
 // four consecutive output features per accumulator group.
 #include "t2t_common.h"
+#include <type_traits>
 
 // work-groups of one projection launch, over all heads (32 per CU)
 #define T2T_PROJ_WGS 8192
@@ -82,6 +83,145 @@ __global__ __launch_bounds__(256) void project_kernel(const uint16_t* __restrict
   }
 }
 
+// D = 128: rows come by LDS DMA, 16 bytes per lane, four whole rows per
+// instruction, into a per-wave double buffer; 16-byte chunk c of row r sits at
+// chunk c ^ (r & 15), so the B-fragment reads (32 rows, one chunk each) are
+// conflict free.  The fp16 outputs of a block are staged in LDS and stored as
+// 1 KB contiguous runs.  Waves work alone (no work-group barrier in the loop).
+// s_waitcnt immediate (gfx9) that waits for vmcnt <= n only
+#define PJ_VMCNT(n) (((n) & 0xf) | (0x7 << 4) | (0xf << 8) | ((((n) >> 4) & 0x3) << 14))
+typedef __attribute__((address_space(3))) void pj_lds_t;
+typedef __attribute__((address_space(1))) void pj_glb_t;
+template <typename T>
+__global__ __launch_bounds__(256, 2) void project_lds_kernel(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ U,
+                                                             uint16_t* __restrict__ out, int N,
+                                                             long long sxh, long long sxn) {
+  constexpr int D = 128, KS = D / 16;
+  __shared__ __attribute__((aligned(1024))) uint16_t sX0[4][32 * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t sX1[4][32 * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sO[4][32 * 32];
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int jl = lane & 31, hh = lane >> 5;
+  const uint16_t* Uh = U + (size_t)h * D * 32;
+  // U (8 KB) staged through the first buffers, then held as fragments
+  {
+    uint16_t* sU = &sX0[0][0];
+    for (int i = threadIdx.x; i < D * 32 / 8; i += 256) ((u32x4*)sU)[i] = ((const u32x4*)Uh)[i];
+  }
+  __syncthreads();
+  u32x4 ua[KS];
+  {
+    const uint16_t* sU = &sX0[0][0];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        ua[s][t] = (uint32_t)sU[(16 * s + 8 * hh + 2 * t) * 32 + jl] |
+                   ((uint32_t)sU[(16 * s + 8 * hh + 2 * t + 1) * 32 + jl] << 16);
+  }
+  __syncthreads();
+  const char* xh = (const char*)(x + (size_t)h * sxh);
+  const size_t rowb = (size_t)sxn * 2;
+  uint16_t* oh = out + (size_t)h * N * 32;
+  const int step = gridDim.x * 4 * 32;
+  // DMA of block r0 into buffer B: instruction i fills rows 4 i .. 4 i + 3
+  auto issue = [&](int r0, auto BUF) {
+    uint16_t* sb = decltype(BUF)::value ? sX1[wave] : sX0[wave];
+    const int rr = lane >> 4, p = lane & 15;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 4 * i + rr;
+      int row = r0 + r;
+      row = row < N ? row : N - 1;
+      const char* src = xh + (size_t)row * rowb + 16 * (p ^ (r & 15));
+      __builtin_amdgcn_global_load_lds((const pj_glb_t*)src, (pj_lds_t*)(sb + i * 512), 16, 0, 0);
+    }
+  };
+  auto body = [&](int r0, auto BUF) {
+    const uint16_t* sb = decltype(BUF)::value ? sX1[wave] : sX0[wave];
+    // the fragment reads in inline assembly: the compiler cannot tell that
+    // the DMA in flight writes the other buffer and would wait for it here
+    // (the explicit vmcnt waits order these reads after their own block's DMA)
+    const uint32_t sbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)sb;
+    u32x4 b[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      asm volatile("ds_read_b128 %0, %1"
+                   : "=v"(b[s])
+                   : "v"(sbase + 2u * (uint32_t)(jl * D + 8 * ((2 * s + hh) ^ (jl & 15)))));
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]), "+v"(b[4]), "+v"(b[5]), "+v"(b[6]),
+                   "+v"(b[7]));
+    f32x16 acc = zero16();
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      if constexpr (T::code == T2T_BF16) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t w = b[s][t];
+          b[s][t] = (uint32_t)bf2h((uint16_t)(w & 0xffff)) | ((uint32_t)bf2h((uint16_t)(w >> 16)) << 16);
+        }
+      }
+      acc = Mfma<F16T>::run(ua[s], b[s], acc);
+    }
+    // outputs through the wave's staging rows (inline assembly for the same
+    // reason; one wave's LDS accesses complete in issue order)
+    const uint32_t obase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)sO[wave];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      u32x2 o;
+      o[0] = (uint32_t)f2h(acc[4 * g + 0]) | ((uint32_t)f2h(acc[4 * g + 1]) << 16);
+      o[1] = (uint32_t)f2h(acc[4 * g + 2]) | ((uint32_t)f2h(acc[4 * g + 3]) << 16);
+      asm volatile("ds_write_b64 %0, %1" ::"v"(obase + 2u * (uint32_t)(jl * 32 + 8 * g + 4 * hh)), "v"(o)
+                   : "memory");
+    }
+    u32x4 ov[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      asm volatile("ds_read_b128 %0, %1"
+                   : "=v"(ov[i])
+                   : "v"(obase + 2u * (uint32_t)((16 * i + (lane >> 2)) * 32 + 8 * (lane & 3)))
+                   : "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ov[0]), "+v"(ov[1]));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = 16 * i + (lane >> 2);
+      if (r0 + r < N) *(u32x4*)(oh + (size_t)(r0 + r) * 32 + 8 * (lane & 3)) = ov[i];
+    }
+  };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  int r0 = (blockIdx.x * 4 + wave) * 32;
+  if (r0 >= N) return;
+  // Vector-memory operations of a wave complete in issue order (gfx9), so
+  // after the next block's 8 DMA loads are issued, "at most 10 outstanding"
+  // (those 8 and the previous block's 2 output stores) means the current
+  // block's loads, issued before both, have landed; "at most 8" on the first
+  // block, before any store.
+  issue(r0, B0{});
+  bool first = true;
+  for (;;) {
+    // buffer 0 holds r0 (in flight); start r0 + step into buffer 1
+    const bool more = r0 + step < N;
+    if (more) issue(r0 + step, B1{});
+    if (!more) __builtin_amdgcn_s_waitcnt(PJ_VMCNT(0));
+    else if (first) __builtin_amdgcn_s_waitcnt(PJ_VMCNT(8));
+    else __builtin_amdgcn_s_waitcnt(PJ_VMCNT(10));
+    first = false;
+    body(r0, B0{});
+    r0 += step;
+    if (!more) break;
+    const bool more2 = r0 + step < N;
+    if (more2) issue(r0 + step, B0{});
+    if (more2) __builtin_amdgcn_s_waitcnt(PJ_VMCNT(10)); else __builtin_amdgcn_s_waitcnt(PJ_VMCNT(0));
+    body(r0, B1{});
+    r0 += step;
+    if (!more2) break;
+  }
+}
+
 template <typename T>
 static int launch_project(const void* x, const void* U, void* out, int H, int N, int D,
                           long long sxh, long long sxn, hipStream_t st) {
@@ -91,7 +231,7 @@ static int launch_project(const void* x, const void* U, void* out, int H, int N,
   dim3 grid(gx, H);
   switch (D) {
     case 128:
-      hipLaunchKernelGGL((project_kernel<T, 128>), grid, dim3(256), 0, st, (const uint16_t*)x,
+      hipLaunchKernelGGL((project_lds_kernel<T>), grid, dim3(256), 0, st, (const uint16_t*)x,
                          (const uint16_t*)U, (uint16_t*)out, N, sxh, sxn);
       break;
     case 64:
