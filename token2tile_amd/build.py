@@ -30,8 +30,10 @@ FLAGS = [
 ]
 
 
-# per-file extra compiler flags
-EXTRA: dict = {}
+# per-file extra compiler flags.  kmeans.hip: MFMA accumulators in VGPRs
+# rather than AGPRs; the assignment's min tree reads all 16 per block, and the
+# AGPR form spent 16 v_accvgpr_read per block on moving them out
+EXTRA: dict = {"kmeans.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def sources():
