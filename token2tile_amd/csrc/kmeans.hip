@@ -18,20 +18,16 @@
 static inline int pad32(int c) { return (c + 31) & ~31; }
 
 // ---------------------------------------------------------------------------
-// assignment.  Transposed MFMA product: centroids on the row axis (A), tokens
-// on the column axis (B), so a lane owns one token and 16 centroids per
-// 32-centroid block, visited in ascending index order.
-//   MODE 0 (kmeans):     d = cnorm + x.(-2c), argmin, ties -> lowest index
-//   MODE 1 (fast_assign): d2 = |x|^2 + (cn2 - 2 x.c); key = (bits(d2) & ~m) | c
+// fast_assign (init_state).  Transposed MFMA product: centroids on the row
+// axis (A), tokens on the column axis (B), so a lane owns one token and 16
+// centroids per 32-centroid block, visited in ascending index order:
+// d2 = |x|^2 + (cn2 - 2 x.c); key = (bits(d2) & ~m) | c, the smallest key wins.
 // ---------------------------------------------------------------------------
-template <int MODE, int D>
-__global__ __launch_bounds__(256) void assign_kernel(const uint16_t* __restrict__ X,
-                                                     const uint16_t* __restrict__ cen,
-                                                     const uint16_t* __restrict__ cprep,
-                                                     const float* __restrict__ cnorm,
-                                                     int32_t* __restrict__ labels, int N, int C,
-                                                     int pin_begin, int pin_label, int ibits,
-                                                     const int32_t* __restrict__ guess) {
+template <int D>
+__global__ __launch_bounds__(256) void fast_assign_kernel(const uint16_t* __restrict__ X,
+                                                          const uint16_t* __restrict__ cen,
+                                                          int32_t* __restrict__ labels, int N,
+                                                          int C, int ibits) {
   constexpr int KS = D / 16;
   __shared__ __attribute__((aligned(16))) uint16_t sC[AS_CHUNK * D];
   __shared__ float sN[AS_CHUNK];
@@ -47,92 +43,28 @@ __global__ __launch_bounds__(256) void assign_kernel(const uint16_t* __restrict_
   for (int s = 0; s < KS; ++s) {
     bx[s] = u32x4{0u, 0u, 0u, 0u};
     if (ok) bx[s] = *(const u32x4*)(xh + (size_t)row * D + 16 * s + 8 * hh);
-    if (MODE == 1) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float a = h2f((uint16_t)(bx[s][t] & 0xffff)), b = h2f((uint16_t)(bx[s][t] >> 16));
-        xsq += a * a + b * b;
-      }
+    for (int t = 0; t < 4; ++t) {
+      const float a = h2f((uint16_t)(bx[s][t] & 0xffff)), b = h2f((uint16_t)(bx[s][t] >> 16));
+      xsq += a * a + b * b;
     }
   }
-  if (MODE == 1) xsq = half_sum(xsq);
+  xsq = half_sum(xsq);
   const uint16_t* ch = cen + (size_t)h * C * D;
   const int Cp = (C + 31) & ~31;
-  float best = __builtin_inff();
-  int bidx = 0;
   int bkey = 0x7fffffff;
-  // MODE 0 pruning bound from a guess: the row's previous label (any value;
-  // used only when it names a centroid).  Its distance, summed here in fp32,
-  // plus a bound on the rounding of that sum and of the MFMA's own (33 terms
-  // in any order: under 2^-18 of the sum of their magnitudes each; 2^-16 is
-  // taken) is strictly above the MFMA distance of the guessed centroid, so
-  // starting the running minimum there changes no label: the result is still
-  // the first centroid, in visiting order, at the minimum MFMA distance.  It
-  // only spares the index search of every block that cannot hold that minimum.
-  if (MODE == 0 && guess && cprep) {
-    const int g = ok ? guess[(size_t)h * N + row] : -1;
-    const bool have = g >= 0 && g < C;
-    float part = 0.f, mag = 0.f;
-    if (have) {
-      const uint16_t* cg = cprep + ((size_t)h * C + g) * D;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const u32x4 cv = *(const u32x4*)(cg + 16 * s + 8 * hh);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float x0 = h2f((uint16_t)(bx[s][t] & 0xffff)), c0 = h2f((uint16_t)(cv[t] & 0xffff));
-          const float x1 = h2f((uint16_t)(bx[s][t] >> 16)), c1 = h2f((uint16_t)(cv[t] >> 16));
-          part = fmaf(x0, c0, part);
-          part = fmaf(x1, c1, part);
-          mag = fmaf(fabsf(x0), fabsf(c0), mag);
-          mag = fmaf(fabsf(x1), fabsf(c1), mag);
-        }
-      }
-    }
-    const float opart = __builtin_bit_cast(float, half_partner(__builtin_bit_cast(uint32_t, part)));
-    const float omag = __builtin_bit_cast(float, half_partner(__builtin_bit_cast(uint32_t, mag)));
-    if (have) {
-      const float cn = cnorm[(size_t)h * C + g];
-      const float d = cn + (hh ? opart + part : part + opart);
-      const float sz = fabsf(cn) + (hh ? omag + mag : mag + omag);
-      best = d + 0x1p-16f * sz + 0x1p-126f;
-      bidx = g;
-    }
-  }
   const int kmask = -(1 << ibits);
   for (int c0 = 0; c0 < Cp; c0 += AS_CHUNK) {
     const int nc = (Cp - c0) < AS_CHUNK ? (Cp - c0) : AS_CHUNK;
     __syncthreads();
-    // stage the chunk: -2c (MODE 0, exact in fp16) or c (MODE 1); padding = 0.
-    // With cprep (MODE 0) the negated centroids and their norms come from
-    // cen_prep_kernel, computed once per launch instead of once per block.
-    if (cprep) {
-      const uint16_t* cph = cprep + (size_t)h * C * D;
-      for (int i = tid; i < nc * D / 8; i += 256) {
-        const int ci = c0 + (i * 8) / D;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (ci < C) v = ((const u32x4*)(cph + (size_t)c0 * D))[i];
-        ((u32x4*)sC)[i] = v;
-      }
-      for (int i = tid; i < nc; i += 256) {
-        const int ci = c0 + i;
-        sN[i] = (ci < C) ? cnorm[(size_t)h * C + ci] : __builtin_inff();
-      }
-      __syncthreads();
-    } else {
+    // stage the chunk (padding = 0) and the squared norms in fp32, summed
+    // sequentially over the dims (each square is exact)
     for (int i = tid; i < nc * D / 8; i += 256) {
       const int ci = c0 + (i * 8) / D;
       u32x4 v = {0u, 0u, 0u, 0u};
       if (ci < C) v = ((const u32x4*)(ch + (size_t)c0 * D))[i];
-      if (MODE == 0) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          v[t] = (uint32_t)f2h(-2.0f * h2f((uint16_t)(v[t] & 0xffff))) |
-                 ((uint32_t)f2h(-2.0f * h2f((uint16_t)(v[t] >> 16))) << 16);
-      }
       ((u32x4*)sC)[i] = v;
     }
-    // squared norms in fp32, sequential over the dims (each square is exact)
     for (int i = tid; i < nc; i += 256) {
       const int ci = c0 + i;
       float s = 0.f;
@@ -146,68 +78,167 @@ __global__ __launch_bounds__(256) void assign_kernel(const uint16_t* __restrict_
       sN[i] = (ci < C) ? s : __builtin_inff();
     }
     __syncthreads();
-    }
     for (int cb = 0; cb < nc / 32; ++cb) {
-      f32x16 acc;
-#pragma unroll
-      for (int a = 0; a < 16; ++a)
-        acc[a] = (MODE == 0) ? sN[cb * 32 + 8 * (a / 4) + 4 * hh + (a % 4)] : 0.f;
+      f32x16 acc = zero16();
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const u32x4 av = *(const u32x4*)(sC + (cb * 32 + jl) * D + 16 * s + 8 * hh);
         acc = Mfma<F16T>::run(av, bx[s], acc);
       }
-      if (MODE == 0) {
-        // the block's minimum by a min3 tree; only a block that improves some
-        // lane's running minimum looks for its lowest index at that value
-        // (accumulator order a is ascending centroid order)
-        auto mn = [](float a, float b) { return __builtin_elementwise_minimum(a, b); };
-        float t8[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) t8[i] = mn(acc[2 * i], acc[2 * i + 1]);
-        const float bmin = mn(mn(mn(t8[0], t8[1]), mn(t8[2], t8[3])),
-                              mn(mn(t8[4], t8[5]), mn(t8[6], t8[7])));
-        if (__ballot(bmin < best) != 0ull) {
-          if (bmin < best) {
-            int ia = 15;
-#pragma unroll
-            for (int a = 14; a >= 0; --a) ia = acc[a] == bmin ? a : ia;
-            best = bmin;
-            bidx = c0 + cb * 32 + 8 * (ia >> 2) + 4 * hh + (ia & 3);
-          }
-        }
-        continue;
-      }
 #pragma unroll
       for (int a = 0; a < 16; ++a) {
         const int ci = c0 + cb * 32 + 8 * (a / 4) + 4 * hh + (a % 4);
-        {
-          const float cn2 = sN[cb * 32 + 8 * (a / 4) + 4 * hh + (a % 4)];
-          const float d2 = xsq + (cn2 - 2.0f * acc[a]);
-          int key = (__builtin_bit_cast(int, d2) & kmask) | ci;
-          if (ci >= C) key = 0x7fffffff;
-          bkey = key < bkey ? key : bkey;
+        const float cn2 = sN[cb * 32 + 8 * (a / 4) + 4 * hh + (a % 4)];
+        const float d2 = xsq + (cn2 - 2.0f * acc[a]);
+        int key = (__builtin_bit_cast(int, d2) & kmask) | ci;
+        if (ci >= C) key = 0x7fffffff;
+        bkey = key < bkey ? key : bkey;
+      }
+    }
+  }
+  const int ok2 = (int)half_partner((uint32_t)bkey);
+  bkey = ok2 < bkey ? ok2 : bkey;
+  if (ok && hh == 0) labels[(size_t)h * N + row] = bkey & ((1 << ibits) - 1);
+}
+
+// ---------------------------------------------------------------------------
+// k-means assignment at rank 32: d = |c|^2 + x.(-2c),
+// argmin, ties to the lowest index.  One 8-wave work-group per 1024 rows, four
+// 32-row blocks per wave, so every centroid fragment and norm read from LDS
+// feeds four MFMA chains; the centroids (-2c and |c|^2 from cen_prep_kernel)
+// are staged in chunks of CMAX rows (34 KB at 512: four work-groups per CU).
+// Centroid row r keeps its 16-byte chunk c at c ^ ((r >> 2) & 3), so the 32
+// rows a fragment read touches fall on distinct banks.
+//
+// Pruning bound from a guess: the row's previous label (the label buffer's
+// old contents, any value; used only when it names a centroid).  Its distance,
+// summed here in fp32, plus a bound on the rounding of that sum and of the
+// MFMA's own (33 terms in any order: under 2^-18 of the sum of their
+// magnitudes each; 2^-16 is taken) is strictly above the MFMA distance of the
+// guessed centroid, so starting the running minimum there changes no label:
+// the result is still the first centroid, in visiting order, at the minimum
+// MFMA distance.  A block then costs a min tree and one compare; only a block
+// whose minimum improves on some lane's running minimum looks for its lowest
+// index at that value.
+// ---------------------------------------------------------------------------
+#define AK_WAVES 8
+#define AK_CHUNK 512
+#define AK_RB 4
+template <int CMAX>
+__global__ __launch_bounds__(AK_WAVES * 64) void assign_km_kernel(
+    const uint16_t* __restrict__ X, const uint16_t* __restrict__ cprep,
+    const float* __restrict__ cnorm, int32_t* __restrict__ labels, int N, int C, int pin_begin,
+    int pin_label, const int32_t* __restrict__ guess) {
+  constexpr int D = 32;
+  __shared__ __attribute__((aligned(16))) uint16_t sC[CMAX * D];
+  __shared__ __attribute__((aligned(16))) float sN[CMAX];
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int jl = lane & 31, hh = lane >> 5;
+  const int Cp = (C + 31) & ~31;
+  const uint16_t* xh = X + (size_t)h * N * D;
+  const int rbase = blockIdx.x * (AK_WAVES * 32 * AK_RB) + wave * 32 * AK_RB + jl;
+  u32x4 bx[AK_RB][2];
+  float best[AK_RB];
+  int bidx[AK_RB];
+#pragma unroll
+  for (int k = 0; k < AK_RB; ++k) {
+    const int row = rbase + 32 * k;
+    const bool ok = row < N;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      bx[k][s] = u32x4{0u, 0u, 0u, 0u};
+      if (ok) bx[k][s] = *(const u32x4*)(xh + (size_t)row * D + 16 * s + 8 * hh);
+    }
+    // pruning bound from the row's previous label
+    best[k] = __builtin_inff();
+    bidx[k] = 0;
+    const int g = (ok && guess) ? guess[(size_t)h * N + row] : -1;
+    const bool have = g >= 0 && g < C;
+    float part = 0.f, mag = 0.f;
+    if (have) {
+      const uint16_t* cg = cprep + ((size_t)h * C + g) * D;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const u32x4 cv = *(const u32x4*)(cg + 16 * s + 8 * hh);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float x0 = h2f((uint16_t)(bx[k][s][t] & 0xffff)), c0 = h2f((uint16_t)(cv[t] & 0xffff));
+          const float x1 = h2f((uint16_t)(bx[k][s][t] >> 16)), c1 = h2f((uint16_t)(cv[t] >> 16));
+          part = fmaf(x0, c0, part);
+          part = fmaf(x1, c1, part);
+          mag = fmaf(fabsf(x0), fabsf(c0), mag);
+          mag = fmaf(fabsf(x1), fabsf(c1), mag);
+        }
+      }
+    }
+    const float opart = __builtin_bit_cast(float, half_partner(__builtin_bit_cast(uint32_t, part)));
+    const float omag = __builtin_bit_cast(float, half_partner(__builtin_bit_cast(uint32_t, mag)));
+    if (have) {
+      const float cn = cnorm[(size_t)h * C + g];
+      const float d = cn + (hh ? opart + part : part + opart);
+      const float sz = fabsf(cn) + (hh ? omag + mag : mag + omag);
+      best[k] = d + 0x1p-16f * sz + 0x1p-126f;
+      bidx[k] = g;
+    }
+  }
+  auto mn = [](float a, float b) { return __builtin_elementwise_minimum(a, b); };
+  const u32x4* cph = (const u32x4*)(cprep + (size_t)h * C * D);
+  for (int c0 = 0; c0 < Cp; c0 += CMAX) {
+  const int nc = Cp - c0 < CMAX ? Cp - c0 : CMAX;
+  if (c0 > 0) __syncthreads();  // every wave is done with the previous chunk
+  for (int i = tid; i < nc * 4; i += AK_WAVES * 64) {
+    const int r = i >> 2, c = i & 3;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (c0 + r < C) v = cph[(size_t)c0 * 4 + i];
+    ((u32x4*)sC)[r * 4 + (c ^ ((r >> 2) & 3))] = v;
+  }
+  for (int i = tid; i < nc; i += AK_WAVES * 64)
+    sN[i] = c0 + i < C ? cnorm[(size_t)h * C + c0 + i] : __builtin_inff();
+  __syncthreads();
+  for (int cb = 0; cb < nc / 32; ++cb) {
+    const int r = cb * 32 + jl;
+    const u32x4* crow = (const u32x4*)sC + r * 4;
+    const u32x4 a0 = crow[(0 + hh) ^ ((r >> 2) & 3)];
+    const u32x4 a1 = crow[(2 + hh) ^ ((r >> 2) & 3)];
+    f32x16 init;
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const float4 nv = *(const float4*)(sN + cb * 32 + 8 * gq + 4 * hh);
+      init[4 * gq + 0] = nv.x;
+      init[4 * gq + 1] = nv.y;
+      init[4 * gq + 2] = nv.z;
+      init[4 * gq + 3] = nv.w;
+    }
+#pragma unroll
+    for (int k = 0; k < AK_RB; ++k) {
+      f32x16 acc = Mfma<F16T>::run(a0, bx[k][0], init);
+      acc = Mfma<F16T>::run(a1, bx[k][1], acc);
+      float t8[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) t8[i] = mn(acc[2 * i], acc[2 * i + 1]);
+      const float bmin = mn(mn(mn(t8[0], t8[1]), mn(t8[2], t8[3])), mn(mn(t8[4], t8[5]), mn(t8[6], t8[7])));
+      if (__ballot(bmin < best[k]) != 0ull) {
+        if (bmin < best[k]) {
+          int ia = 15;
+#pragma unroll
+          for (int a = 14; a >= 0; --a) ia = acc[a] == bmin ? a : ia;
+          best[k] = bmin;
+          bidx[k] = c0 + cb * 32 + 8 * (ia >> 2) + 4 * hh + (ia & 3);
         }
       }
     }
   }
-  int lab;
-  if (MODE == 0) {
-    const float ob = __builtin_bit_cast(float, half_partner(__builtin_bit_cast(uint32_t, best)));
-    const int oi = (int)half_partner((uint32_t)bidx);
-    if (ob < best || (ob == best && oi < bidx)) {
-      best = ob;
-      bidx = oi;
-    }
-    lab = bidx;
-  } else {
-    const int ok2 = (int)half_partner((uint32_t)bkey);
-    bkey = ok2 < bkey ? ok2 : bkey;
-    lab = bkey & ((1 << ibits) - 1);
   }
-  if (ok && hh == 0) {
-    if (row >= pin_begin) lab = pin_label;
-    labels[(size_t)h * N + row] = lab;
+#pragma unroll
+  for (int k = 0; k < AK_RB; ++k) {
+    const float ob = __builtin_bit_cast(float, half_partner(__builtin_bit_cast(uint32_t, best[k])));
+    const int oi = (int)half_partner((uint32_t)bidx[k]);
+    int lab = bidx[k];
+    if (ob < best[k] || (ob == best[k] && oi < bidx[k])) lab = oi;
+    const int row = rbase + 32 * k;
+    if (row < N && hh == 0) labels[(size_t)h * N + row] = row >= pin_begin ? pin_label : lab;
   }
 }
 
@@ -581,8 +612,8 @@ extern "C" size_t t2t_kmm_ws_bytes(int H, int N, int CQ, int CK) {
 }
 
 // -2c (exact in fp16) and the fp32 squared norm of every centroid, summed
-// sequentially over the dims (each square is exact), as assign_kernel's
-// MODE 0 staging computes them
+// sequentially over the dims (each square is exact): the operands of
+// assign_km_kernel
 __global__ __launch_bounds__(256) void cen_prep_kernel(const uint16_t* __restrict__ cen,
                                                        uint16_t* __restrict__ cprep,
                                                        float* __restrict__ cnorm, int C) {
@@ -604,9 +635,9 @@ static int launch_assign_km(const void* X, const void* cen, int32_t* lab, int H,
                             const int32_t* guess, hipStream_t st) {
   hipLaunchKernelGGL(cen_prep_kernel, dim3(cdiv(C, 256), H), dim3(256), 0, st,
                      (const uint16_t*)cen, cprep, cnorm, C);
-  hipLaunchKernelGGL((assign_kernel<0, KM_R>), dim3(cdiv(N, 128), H), dim3(256), 0, st,
-                     (const uint16_t*)X, (const uint16_t*)cen, (const uint16_t*)cprep,
-                     (const float*)cnorm, lab, N, C, pin_begin, pin_label, 0, guess);
+  hipLaunchKernelGGL(assign_km_kernel<AK_CHUNK>, dim3(cdiv(N, AK_WAVES * 32 * AK_RB), H),
+                     dim3(AK_WAVES * 64), 0, st, (const uint16_t*)X, (const uint16_t*)cprep,
+                     (const float*)cnorm, lab, N, C, pin_begin, pin_label, guess);
   return t2t_check_launch("assign");
 }
 
@@ -818,17 +849,14 @@ extern "C" int t2t_fast_assign(const void* x, const void* c, int32_t* labels, in
   while ((1 << ibits) < C) ++ibits;
   const dim3 g(cdiv(N, 128), H);
   if (D == 32)
-    hipLaunchKernelGGL((assign_kernel<1, 32>), g, dim3(256), 0, st, (const uint16_t*)x,
-                       (const uint16_t*)c, (const uint16_t*)nullptr, (const float*)nullptr, labels, N, C,
-                       N + 1, 0, ibits, (const int32_t*)nullptr);
+    hipLaunchKernelGGL((fast_assign_kernel<32>), g, dim3(256), 0, st, (const uint16_t*)x,
+                       (const uint16_t*)c, labels, N, C, ibits);
   else if (D == 64)
-    hipLaunchKernelGGL((assign_kernel<1, 64>), g, dim3(256), 0, st, (const uint16_t*)x,
-                       (const uint16_t*)c, (const uint16_t*)nullptr, (const float*)nullptr, labels, N, C,
-                       N + 1, 0, ibits, (const int32_t*)nullptr);
+    hipLaunchKernelGGL((fast_assign_kernel<64>), g, dim3(256), 0, st, (const uint16_t*)x,
+                       (const uint16_t*)c, labels, N, C, ibits);
   else
-    hipLaunchKernelGGL((assign_kernel<1, 128>), g, dim3(256), 0, st, (const uint16_t*)x,
-                       (const uint16_t*)c, (const uint16_t*)nullptr, (const float*)nullptr, labels, N, C,
-                       N + 1, 0, ibits, (const int32_t*)nullptr);
+    hipLaunchKernelGGL((fast_assign_kernel<128>), g, dim3(256), 0, st, (const uint16_t*)x,
+                       (const uint16_t*)c, labels, N, C, ibits);
   T2T_LAUNCH_CHECK("fast_assign");
   return T2T_OK;
 }
