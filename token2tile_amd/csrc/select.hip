@@ -129,6 +129,9 @@ __device__ inline uint32_t key_pair(uint32_t x) {
 // or high (i odd) half of kp[i / 2].
 // cluster of slot i of lane l
 __device__ inline int slot_cluster(int i, int l) { return 512 * (i >> 3) + 8 * l + (i & 7); }
+// column of cluster c in a staged key row whose 16-byte chunks are XOR
+// swizzled by rsw (the row index mod 16)
+__device__ inline int key_col(int c, int rsw) { return 8 * ((c >> 3) ^ rsw) + (c & 7); }
 __device__ inline int key_at(const uint32_t (&kp)[16], int i) {
   return (int)(int16_t)(uint16_t)((i & 1) ? kp[i >> 1] >> 16 : kp[i >> 1] & 0xffffu);
 }
@@ -262,8 +265,8 @@ __device__ inline uint32_t select_bits(const uint32_t (&kp)[16], const int* ssz,
   return gt | (tie & upto);
 }
 
-// Single-pass crossing search in a window of 512 consecutive keys [lo, lo +
-// 512) placed around the previous row's crossing key.  Only the lane's keys
+// Single-pass crossing search in a window of SEL_WIN consecutive keys [lo,
+// lo + SEL_WIN) placed around the previous row's crossing key.  Only the lane's keys
 // at or above lo are visited (a few per lane): a key in the window adds
 // (size << 12) | 1 to its own bin of a wave-private LDS histogram, a key above
 // it adds its size to a register sum; keys below lo are not touched.  The
@@ -273,9 +276,10 @@ __device__ inline uint32_t select_bits(const uint32_t (&kp)[16], const int* ssz,
 // crossing key, the weight above it and the weight and count of its clusters
 // without the two radix passes (returns 0); otherwise it returns 1 (crossing
 // above the window) or -1 (below it).
-#define SEL_WIN 512
+#define SEL_WIN 448
+#define SEL_WPL (SEL_WIN / 64)  // window bins per lane
 #define SEL_WHIST SEL_WIN  // window bins (the radix fallback uses the first 320)
-__device__ inline int window_cross(const uint32_t (&kp)[16], const uint16_t* krow, const int* ssz,
+__device__ inline int window_cross(const uint32_t (&kp)[16], const uint16_t* krow, int rsw, const int* ssz,
                                    int* hist, int ns, int lo, int* vstar, int* wgt, int* weq,
                                    int* ntie, uint32_t* bits, int* bits_ok) {
   const int l = __lane_id();
@@ -284,8 +288,8 @@ __device__ inline int window_cross(const uint32_t (&kp)[16], const uint16_t* kro
   // reads below need no memory wait between them: the compiler barriers
   // (lds_order) only keep the compiler from reordering them.
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-    *(u32x4*)(hist + 4 * (l + 64 * i)) = u32x4{0u, 0u, 0u, 0u};
+  for (int i = 0; i < (SEL_WIN + 255) / 256; ++i)
+    if (l + 64 * i < SEL_WIN / 4) *(u32x4*)(hist + 4 * (l + 64 * i)) = u32x4{0u, 0u, 0u, 0u};
   lds_order();
   // the lane's keys at or above the window's base, as a mask
   uint32_t m = keys_ge(kp, lo);
@@ -308,7 +312,7 @@ __device__ inline int window_cross(const uint32_t (&kp)[16], const uint16_t* kro
     }
 #pragma unroll
     for (int it = 0; it < SEL_CAND1; ++it) {
-      d1[it] = (int)(int16_t)krow[c[it]] - lo;
+      d1[it] = (int)(int16_t)krow[key_col(c[it], rsw)] - lo;
       sz[it] = ssz[c[it]];
     }
 #pragma unroll
@@ -331,7 +335,7 @@ __device__ inline int window_cross(const uint32_t (&kp)[16], const uint16_t* kro
     int d[SEL_CAND], sz[SEL_CAND];
 #pragma unroll
     for (int it = 0; it < SEL_CAND; ++it) {
-      d[it] = (int)(int16_t)krow[c[it]] - lo;
+      d[it] = (int)(int16_t)krow[key_col(c[it], rsw)] - lo;
       sz[it] = ssz[c[it]];
     }
 #pragma unroll
@@ -341,12 +345,12 @@ __device__ inline int window_cross(const uint32_t (&kp)[16], const uint16_t* kro
     }
   }
   lds_order();
-  // lane l scans bins 511 - 8 l .. 504 - 8 l (descending keys)
-  int raw[8];
+  // lane l scans its SEL_WPL bins, from the top (descending keys)
+  int raw[SEL_WPL];
   int s = 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    raw[i] = hist[SEL_WIN - 1 - 8 * l - i];
+  for (int i = 0; i < SEL_WPL; ++i) {
+    raw[i] = hist[SEL_WIN - 1 - SEL_WPL * l - i];
     s += raw[i] >> 12;
   }
   const int above = wave_sum(aw);
@@ -362,10 +366,10 @@ __device__ inline int window_cross(const uint32_t (&kp)[16], const uint16_t* kro
     int cum = ex;
     bool done = false;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < SEL_WPL; ++i) {
       const int w = raw[i] >> 12;
       if (!done && cum + w >= ns) {
-        bin = SEL_WIN - 1 - 8 * l - i;
+        bin = SEL_WIN - 1 - SEL_WPL * l - i;
         ab = cum;
         raw_b = raw[i];
         done = true;
@@ -482,24 +486,31 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Fused scoring + selection: the scores never leave the chip.  One 8-wave
-// work-group per CU takes batches of 32 consecutive sorted rows: every wave
-// computes the scores of the batch against 256 of the centroids on MFMA, with
+// Fused scoring + selection: the scores never leave the chip.  One 12-wave
+// work-group per CU (three waves per SIMD) takes batches of 32 consecutive
+// sorted rows: every wave computes the scores of the batch against 160 or 192
+// of the centroids on MFMA, with
 // the instruction, operand split and fp16 rounding of score_kernel (so the
 // scores, and the selection, are bit-identical to the unfused path), and
 // stores the ordered keys in LDS; then the waves select the rows, taking
-// them one at a time from a counter.  A row is searched in a 512-key window
+// them one at a time from a counter.  A row is searched in a 448-key window
 // around the previous row's crossing (window_cross: a few keys per lane, one
 // histogram pass), then in the window above or below it, and by the radix
 // passes only when both miss (a few rows in 10^4 at 720p).  A work-group
 // walks 16 batches (512 rows): the cluster sizes it loads once are amortised
 // over them, and the next batch's query rows load while the current batch is
-// being selected.  The wave's centroid fragments are loaded once and held.
+// being selected.  LDS: the batch's keys (128 KB; 16-byte chunks XOR
+// swizzled by row instead of padded), twelve 1.75 KB window histograms and the
+// cluster sizes.  The centroid fragments are reloaded from L2 per batch: held
+// across batches they would push the kernel past the 168 registers of three
+// waves per SIMD.
 // ---------------------------------------------------------------------------
-#define SF_WAVES 8
+#define SF_WAVES 12
 #define SF_ROWS 32
 #define SF_BATCHES 16
-#define SF_PITCH (SEL_NC + 8)  // halves per LDS key row (16-byte aligned rows)
+#define SF_PITCH SEL_NC  // halves per LDS key row (chunks swizzled by row, no padding)
+#define SF_TILES 6       // most 32-centroid score tiles a wave holds (64 tiles over 12 waves)
+
 
 __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
     const uint16_t* __restrict__ QU, const uint16_t* __restrict__ cks,
@@ -534,9 +545,13 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
   int ns = *ns_dev;
   ns = ns < 1 ? 1 : ns;
   ns = ns > ktot ? ktot : ns;
-  // centroid fragments of the wave's 256 centroids (the A operands of
-  // score_kernel: row 32 cb + jl, dims 8 hh .. and 16 + 8 hh ..)
-  const uint16_t* ch = cks + ((size_t)h * SEL_NC + 256 * wv + jl) * 32 + 8 * hh;
+  // centroid fragments of the wave's score tiles (the A operands of
+  // score_kernel: row 32 cb + jl, dims 8 hh .. and 16 + 8 hh ..): waves 0-3
+  // take 6 of the 64 tiles, waves 4-11 take 5
+  const int wv_u = __builtin_amdgcn_readfirstlane(wv);
+  const int t0 = wv_u < 4 ? 6 * wv_u : 24 + 5 * (wv_u - 4);
+  const int ntl = wv_u < 4 ? 6 : 5;
+  const uint16_t* ch = cks + ((size_t)h * SEL_NC + 32 * t0 + jl) * 32 + 8 * hh;
   const int32_t* qp = qperm + (size_t)h * N;
   const uint16_t* qh = QU + (size_t)h * N * 32;
   int32_t* uh = unip + (size_t)h * CQ * (SEL_NC / 32);
@@ -557,22 +572,29 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
   };
   u32x4 b0, b1;
   load_rows(base, b0, b1);
-  // the wave's centroid fragments, held for all batches
-  u32x4 ca0[8], ca1[8];
+  auto load_ca = [&](u32x4 (&ca0)[SF_TILES], u32x4 (&ca1)[SF_TILES]) {
 #pragma unroll
-  for (int cb = 0; cb < 8; ++cb) {
-    ca0[cb] = *(const u32x4*)(ch + cb * 32 * 32);
-    ca1[cb] = *(const u32x4*)(ch + cb * 32 * 32 + 16);
-  }
+    for (int cb = 0; cb < SF_TILES; ++cb) {
+      ca0[cb] = ca1[cb] = u32x4{0u, 0u, 0u, 0u};
+      if (cb < ntl) {
+        ca0[cb] = *(const u32x4*)(ch + cb * 32 * 32);
+        ca1[cb] = *(const u32x4*)(ch + cb * 32 * 32 + 16);
+      }
+    }
+  };
+
   if (threadIdx.x < 2) sNext[threadIdx.x] = 0;
   for (int c = threadIdx.x; c < SEL_NC; c += SF_WAVES * 64) sSz[c] = kcounts[(size_t)h * SEL_NC + c];
   for (int b = 0; b < SF_BATCHES; ++b) {
     const int j0 = base + SF_ROWS * b;
     if (j0 >= lim) break;
     {  // scores of rows j0 .. j0 + 31 against the wave's centroids -> keys in LDS
-      uint16_t* krow = sKey + jl * SF_PITCH + 256 * wv + 4 * hh;
+      uint16_t* krow = sKey + jl * SF_PITCH + 4 * hh;
+      u32x4 ca0[SF_TILES], ca1[SF_TILES];  // reloaded (from L2) for each batch
+      load_ca(ca0, ca1);
 #pragma unroll
-      for (int cb = 0; cb < 8; ++cb) {
+      for (int cb = 0; cb < SF_TILES; ++cb) {
+        if (cb >= ntl) break;  // wave-uniform
         f32x16 sc = zero16();
         sc = Mfma<F16T>::run(ca0[cb], b0, sc);
         sc = Mfma<F16T>::run(ca1[cb], b1, sc);
@@ -584,7 +606,7 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
           o[1] = Pk<F16T>::pack(sc[4 * g + 2], sc[4 * g + 3]);
 #pragma unroll
           for (int w = 0; w < 2; ++w) o[w] = key_pair(o[w]);  // ordered keys of both halves
-          *(u32x2*)(krow + 32 * cb + 8 * g) = o;
+          *(u32x2*)(krow + key_col(32 * (t0 + cb) + 8 * g, jl & 15)) = o;
         }
       }
     }
@@ -623,9 +645,10 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
       }
       uint32_t kp[16];
       const uint16_t* kr = sKey + r * SF_PITCH;
+      const int rsw = r & 15;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const u32x4 v = *(const u32x4*)(kr + 512 * g + 8 * l);
+        const u32x4 v = *(const u32x4*)(kr + key_col(512 * g + 8 * l, rsw));
 #pragma unroll
         for (int q = 0; q < 4; ++q) kp[4 * g + q] = v[q];
       }
@@ -637,12 +660,12 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
       uint32_t bits = 0;
       if (klo != SEL_NO_BOUND) {
         const int lo = vstar - SEL_WIN / 2;
-        where = window_cross(kp, kr, sSz, hist, ns, lo, &vs, &wgt, &weq, &ntie, &bits, &bits_ok);
+        where = window_cross(kp, kr, rsw, sSz, hist, ns, lo, &vs, &wgt, &weq, &ntie, &bits, &bits_ok);
         if (where > 0)  // the crossing is above the window: the window above it
-          where = window_cross(kp, kr, sSz, hist, ns, lo + SEL_WIN, &vs, &wgt, &weq, &ntie, &bits,
+          where = window_cross(kp, kr, rsw, sSz, hist, ns, lo + SEL_WIN, &vs, &wgt, &weq, &ntie, &bits,
                                &bits_ok);
         else if (where < 0)  // below it: the window below
-          where = window_cross(kp, kr, sSz, hist, ns, lo - SEL_WIN, &vs, &wgt, &weq, &ntie, &bits,
+          where = window_cross(kp, kr, rsw, sSz, hist, ns, lo - SEL_WIN, &vs, &wgt, &weq, &ntie, &bits,
                                &bits_ok);
       }
       if (where != 0 || klo == SEL_NO_BOUND) {
