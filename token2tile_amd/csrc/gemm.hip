@@ -195,27 +195,23 @@ __global__ __launch_bounds__(256, 2) void project_lds_kernel(const uint16_t* __r
   using B1 = std::integral_constant<int, 1>;
   int r0 = (blockIdx.x * 4 + wave) * 32;
   if (r0 >= N) return;
-  // Vector-memory operations of a wave complete in issue order (gfx9), so
-  // after the next block's 8 DMA loads are issued, "at most 10 outstanding"
-  // (those 8 and the previous block's 2 output stores) means the current
-  // block's loads, issued before both, have landed; "at most 8" on the first
-  // block, before any store.
+  // After the next block's 8 DMA loads are issued, "at most 8 outstanding"
+  // means every older vector-memory operation of the wave has completed: the
+  // current block's loads and the previous block's output stores (waiting for
+  // those stores as well costs nothing measurable, and needs no assumption on
+  // how loads and stores are ordered)
   issue(r0, B0{});
-  bool first = true;
   for (;;) {
     // buffer 0 holds r0 (in flight); start r0 + step into buffer 1
     const bool more = r0 + step < N;
     if (more) issue(r0 + step, B1{});
-    if (!more) __builtin_amdgcn_s_waitcnt(PJ_VMCNT(0));
-    else if (first) __builtin_amdgcn_s_waitcnt(PJ_VMCNT(8));
-    else __builtin_amdgcn_s_waitcnt(PJ_VMCNT(10));
-    first = false;
+    if (more) __builtin_amdgcn_s_waitcnt(PJ_VMCNT(8)); else __builtin_amdgcn_s_waitcnt(PJ_VMCNT(0));
     body(r0, B0{});
     r0 += step;
     if (!more) break;
     const bool more2 = r0 + step < N;
     if (more2) issue(r0 + step, B0{});
-    if (more2) __builtin_amdgcn_s_waitcnt(PJ_VMCNT(10)); else __builtin_amdgcn_s_waitcnt(PJ_VMCNT(0));
+    if (more2) __builtin_amdgcn_s_waitcnt(PJ_VMCNT(8)); else __builtin_amdgcn_s_waitcnt(PJ_VMCNT(0));
     body(r0, B1{});
     r0 += step;
     if (!more2) break;
