@@ -58,6 +58,50 @@ def test_project_f16_bf16(dev):
     assert within_ulp(outb, O.project(xr, U))
 
 
+@pytest.mark.parametrize("N", [1, 31, 33, 4097])
+def test_project_edge_rows_and_strides(dev, N):
+    """Row counts around the 32-row blocks of the staged projection, and the
+    token-major view that the backend passes (rows H * 128 apart)."""
+    from token2tile_amd import ops
+    rng = np.random.default_rng(100 + N)
+    H = 3
+    x = rng.normal(0, 1, (H, N, 128)).astype(np.float16)
+    U = (rng.normal(0, 1, (H, 128, 32)) / 8).astype(np.float16)
+    want = O.project(x, U)
+    assert within_ulp(c(ops.project(g(x, dev), g(U, dev))), want)
+    tm = g(np.ascontiguousarray(x.transpose(1, 0, 2)), dev)     # [N, H, 128]
+    assert within_ulp(c(ops.project(tm.transpose(0, 1), g(U, dev))), want)
+
+
+@pytest.mark.parametrize("C", [20, 600])
+def test_kmeans_assignment_small_and_chunked_centroid_counts(dev, C):
+    """Key clusters fewer than one 32-row block, and more than one 512-row
+    staging chunk (not a multiple of 32): near-argmin labels, and the same
+    outputs whatever the label buffers held."""
+    from token2tile_amd import ops
+    rng = np.random.default_rng(200 + C)
+    H, N, CQ = 2, 3000, 40
+    QU = rng.normal(0, 1, (H, N, 32)).astype(np.float16)
+    KU = rng.normal(0, 1, (H, N, 32)).astype(np.float16)
+    cq0 = QU[:, rng.choice(N, CQ, replace=False)].copy()
+    ck0 = KU[:, rng.choice(N, C, replace=False)].copy()
+    V = rng.normal(0, 1, (H, N, 128)).astype(np.float16)
+    args = [g(a, dev) for a in (QU, KU, V, cq0, ck0)]
+    base = ops.kmm_run(*args)
+    klab = c(base["klab"])
+    d = O.assign_distances(KU, ck0)
+    dmin = d.min(-1)
+    mine = np.take_along_axis(d, klab[..., None].astype(np.int64), -1)[..., 0]
+    assert np.all(mine - dmin <= 1e-4 * (1 + np.abs(dmin)))
+    assert (klab != O.assign(KU, ck0)).mean() < 1e-3
+    out = {"klab": g(((klab + 3) % C).astype(np.int32), dev),
+           "qlab": g(rng.integers(-5, CQ + 5, (H, N)).astype(np.int32), dev)}
+    again = ops.kmm_run(*args, out=out)
+    for k_, v_ in base.items():
+        if v_ is not None:
+            assert torch.equal(v_, again[k_]), k_
+
+
 def test_score_and_finalize(dev):
     from token2tile_amd import ops
     rng = np.random.default_rng(1)
