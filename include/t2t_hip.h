@@ -194,7 +194,7 @@ int t2t_tile_attn_exact(const void* q, const void* kp, const void* vp, int dtype
                         const int32_t* plan, void* attn_out, float* lse,
                         int H, int N, int CQ, void* stream);
 /* Bytes of the centroid tile image (cks and transposed sumv in the layout
- * the residual kernel stages into LDS), H x 32 tiles of 20480 bytes. */
+ * the residual kernel stages into LDS), H x 32 tiles of 22528 bytes. */
 size_t t2t_centroid_tiles_bytes(int H);
 /* Workspace bytes of t2t_tail_merge (the centroid tile image). */
 size_t t2t_tail_merge_ws_bytes(int H);

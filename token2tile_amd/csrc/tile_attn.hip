@@ -244,7 +244,9 @@ typedef __attribute__((address_space(1))) void glb_void_t;
 //   sVt [128 dims][64 keys]: the 4-key granules a lane feeds to one MFMA
 //     (g = 4 m + h and 4 m + 2 + h) are stored side by side, so the operand is
 //     one 16-byte read: granule g sits in 16-byte unit (g & ~3) / 2 + (g & 1),
-//     half (g >> 1) & 1, and the unit is XOR-swizzled by ((d >> 1) ^ (d >> 4)) & 7
+//     half (g >> 1) & 1.  Rows are padded to 144 bytes: 16 lanes reading one
+//     unit of 16 consecutive dims start on banks 36 d mod 64, all distinct,
+//     and every operand of a lane is one base address plus a constant.
 __device__ inline int sk_off(int row, int chunk) { return row * 128 + 8 * (chunk ^ (row & 15)); }
 // sV [64 keys][128 dims], row-major, read only by the transposing reads: 16-byte
 // chunk c of key r lives at chunk c ^ sv_swz(r).  One such read has the 32 lanes
@@ -253,8 +255,8 @@ __device__ inline int sk_off(int row, int chunk) { return row * 128 + 8 * (chunk
 // on all 64 banks exactly once.  (The K swizzle, r & 15, would overlap r % 4 with
 // chunk bits 0-1 and leave the half-wave on 16 banks: 4-way conflicts.)
 __device__ inline int sv_swz(int row) { return (row & 3) << 2; }
-__device__ inline int vt_swz(int dim) { return ((dim >> 1) ^ (dim >> 4)) & 7; }
-__device__ inline int vt_unit_off(int dim, int unit) { return dim * 64 + 8 * (unit ^ vt_swz(dim)); }
+#define VT_PITCH 72  // halves per sVt row: 64 keys + one unit of padding
+__device__ inline int vt_unit_off(int dim, int unit) { return dim * VT_PITCH + 8 * unit; }
 __device__ inline int vt_gran_off(int dim, int g) {
   return vt_unit_off(dim, ((g & ~3) >> 1) + (g & 1)) + 4 * ((g >> 1) & 1);
 }
@@ -707,10 +709,12 @@ static void launch_attn(const void* q, const void* kp, const void* vp, const int
 //   [0, 4096)      cks rows, 64 x 32 halves; 16-byte chunk c of row r sits at
 //                  chunk c ^ ((r >> 2) & 3), so the MFMA operand reads of 16
 //                  consecutive rows hit distinct banks
-//   [4096, 20480)  sumv transposed, 128 dims x 64 centroids in the sVt layout
+//   [4096, 22528)  sumv transposed, 128 dims x 64 centroids in the sVt layout
+//                  (the padding unit of each row is never written or read)
 #define RT_TILES (TA_CK / TL_CT)
-#define RT_BYTES 20480
+#define RT_BYTES (4096 + 128 * VT_PITCH * 2)
 #define RT_HALVES (RT_BYTES / 2)
+static_assert(RT_BYTES % 1024 == 0, "the staging moves 1 KB per wave and instruction");
 __device__ inline int rc_off(int r, int c) { return r * 32 + 8 * (c ^ ((r >> 2) & 3)); }
 
 __global__ __launch_bounds__(256) void centroid_tiles_kernel(const uint16_t* __restrict__ cks,
@@ -745,7 +749,7 @@ __global__ __launch_bounds__(256) void centroid_tiles_kernel(const uint16_t* __r
 // read from attn_out (sorted order, SRC_SORTED) or from the original rows of
 // out, and the merged result is written to the original rows of out.
 template <typename T, bool SRC_SORTED>
-__global__ __launch_bounds__(256, 2) void resid_kernel(
+__global__ __launch_bounds__(256, 3) void resid_kernel(
     const uint16_t* __restrict__ exact, const float* __restrict__ lse2v,
     const uint16_t* __restrict__ QU, const uint16_t* __restrict__ tiles,
     const int32_t* __restrict__ kcounts, const uint32_t* __restrict__ unip,
@@ -758,8 +762,11 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
   // half are contiguous: centroid 64 t + 32 kb + 8 j + 4 hh + e sits at
   // 64 t + 32 kb + 16 hh + 4 j + e
   __shared__ __attribute__((aligned(16))) uint16_t sCnt[TA_CK];
+  // row n of sMask: -inf where bit e of n is set, else 0 (the union mask of
+  // four consecutive centroids)
+  __shared__ __attribute__((aligned(16))) float sMask[16 * 4];
   const int h = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int jl = lane & 31, hh = lane >> 5;
   const int row = blockIdx.x * 128 + wave * 32 + jl;  // sorted position
   const bool ok = row < N;
@@ -774,10 +781,16 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
   const char* th = (const char*)(tiles + (size_t)h * RT_TILES * RT_HALVES) + wave * 1024 + lane * 16;
   auto issue = [&](int tc, auto BUF) {
     uint16_t* sb = decltype(BUF)::value ? sT1 : sT0;
+    // 1 KB per wave and instruction; the image's last 2 KB go to waves 0 and 1
+    const char* src = th + (size_t)tc * RT_BYTES;
 #pragma unroll
     for (int i = 0; i < RT_BYTES / 4096; ++i)
-      __builtin_amdgcn_global_load_lds((const glb_void_t*)(th + (size_t)tc * RT_BYTES + i * 4096),
+      __builtin_amdgcn_global_load_lds((const glb_void_t*)(src + i * 4096),
                                        (lds_void_t*)((char*)sb + i * 4096 + wave * 1024), 16, 0, 0);
+    if (wave < (RT_BYTES % 4096) / 1024)
+      __builtin_amdgcn_global_load_lds((const glb_void_t*)(src + (RT_BYTES / 4096) * 4096),
+                                       (lds_void_t*)((char*)sb + (RT_BYTES / 4096) * 4096 + wave * 1024),
+                                       16, 0, 0);
   };
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
@@ -788,6 +801,7 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
     const int pos = (c & ~31) + 16 * ((c >> 2) & 1) + 4 * ((c >> 3) & 3) + (c & 3);
     sCnt[pos] = F16T::from_f((float)kcounts[(size_t)h * TA_CK + c]);
   }
+  if (tid < 64) sMask[tid] = (((tid >> 2) >> (tid & 3)) & 1) ? -__builtin_inff() : 0.f;
   uint32_t uw0 = ur[0], uw1 = ur[1];
   const float L2E = 1.4426950408889634f;
   float m2 = -1.0e30f, phi = 0.f;
@@ -797,6 +811,21 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
+  // accumulator input of a half's score MFMA: nibble j of the lane's union
+  // bits (elements 4 j .. 4 j + 3; element a <-> bit 8 (a / 4) + a % 4 after
+  // the shift by 4 hh) selects a row of sMask, 0 or -inf
+  auto mask_init = [&](uint32_t uword) {
+    const uint32_t u4 = ((uword >> (4 * hh)) << 4) & 0xf0f0f0f0u;
+    f32x16 S;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 mv = *(const f32x4*)((const char*)sMask + ((u4 >> (8 * j)) & 0xffu));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) S[4 * j + e] = mv[e];
+    }
+    return S;
+  };
+  f32x16 Snext = mask_init(uw0);
   auto body = [&](int tc, auto BUF) {
     constexpr int buf = decltype(BUF)::value;
     const uint16_t* sb = buf ? sT1 : sT0;
@@ -806,40 +835,28 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
       nw0 = ur[2 * tc + 2];
       nw1 = ur[2 * tc + 3];
     }
-    // per 32-centroid half kb: fp16 scores of the lane's query against
-    // centroids 32 kb + 8 (a / 4) + 4 hh + a % 4, as pairs, with the union's
-    // centroids at -inf (the union bit spread to an all-ones / zero half and
-    // one bitfield insert; the max runs on the packed pairs and the exponent
-    // argument reads the fp16 halves directly, v_fma_mix_f32); then the
-    // running max, the exponentials and P V of the half.  Working a half at a
-    // time keeps the live scores and P fragments small.
+    // per 32-centroid half kb: scores of the lane's query against centroids
+    // 32 kb + 8 (a / 4) + 4 hh + a % 4 (element a of S), the union's
+    // centroids at -inf; then the exponentials and P V of the half.  Working
+    // a half at a time keeps the live scores and P fragments small.
     const uint16_t* vt = sb + 2048;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int r = 32 * kb + jl;
-      f32x16 S = zero16();
-      S = Mfma<F16T>::run(*(const u32x4*)(sb + rc_off(r, hh)), qu0, S);
-      S = Mfma<F16T>::run(*(const u32x4*)(sb + rc_off(r, 2 + hh)), qu1, S);
-      const uint32_t u = (kb ? uw1 : uw0) >> (4 * hh);  // element a <-> bit 8 (a / 4) + a % 4
-      // pair p = a / 2 reads bits b and b + 1, b = 8 (p / 2) + 2 (p % 2); pairs g
-      // and g + 4 (b and b + 16) share two shifted copies of u: X has bit b at
-      // 15 and b + 16 at 31, Y bits b + 1 and b + 17 there, and v_perm_b32's
-      // sign-replicating selectors (8: X[15], 9: X[31], 10: Y[15], 11: Y[31])
-      // spread each bit over its fp16 half
-      uint32_t mk[8];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int b = 8 * (g >> 1) + 2 * (g & 1);
-        const uint32_t X = u << (15 - b), Y = u << (14 - b);
-        mk[g] = __builtin_amdgcn_perm(Y, X, 0x0a0a0808u);
-        mk[g + 4] = __builtin_amdgcn_perm(Y, X, 0x0b0b0909u);
-      }
+      // the union mask enters as the score MFMA's accumulator input, loaded
+      // one half ahead
+      f32x16 S = Snext;
+      Snext = mask_init(kb ? nw0 : uw1);
+      const u32x4 ca0 = *(const u32x4*)(sb + rc_off(r, hh));
+      const u32x4 ca1 = *(const u32x4*)(sb + rc_off(r, 2 + hh));
+      S = Mfma<F16T>::run(ca0, qu0, S);
+      S = Mfma<F16T>::run(ca1, qu1, S);
+      // fp16 scores (the reference rounds each centroid score to fp16), the
+      // masked ones still -inf
       f16x2 sp[8];
 #pragma unroll
-      for (int a = 0; a < 16; a += 2) {
-        const uint32_t pk = Pk<F16T>::pack(S[a], S[a + 1]);
-        sp[a / 2] = __builtin_bit_cast(f16x2, bfi(mk[a / 2], 0xfc00fc00u, pk));
-      }
+      for (int a = 0; a < 16; a += 2)
+        sp[a / 2] = __builtin_bit_cast(f16x2, Pk<F16T>::pack(S[a], S[a + 1]));
       // weights against the current max, without taking this half's max: the
       // exponentials scale exactly, so m2 only has to keep the fp16 P in
       // range.  The count-weighted sum of the half bounds the weight of every
@@ -848,6 +865,7 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
       // m2 = -1e30, or scores far above the earlier ones) is redone with m2
       // moved past its max (the reference's lazy max), the sums so far
       // rescaled.  An empty cluster's weight can pass unseen only while finite.
+      // The exponent argument reads the fp16 halves directly (v_fma_mix_f32).
       u32x4 pb[2];
       const u32x4* cw = (const u32x4*)(sCnt + TL_CT * tc + 32 * kb + 16 * hh);
       const u32x4 cn0 = cw[0], cn1 = cw[1];
@@ -892,14 +910,14 @@ __global__ __launch_bounds__(256, 2) void resid_kernel(
         pt = expo(-m2 * L2E);
       }
       phi += pt;
+      // the eight V^T fragments of the half are read together, so their LDS
+      // latency is paid once rather than before every MFMA
+      u32x4 vf[8];
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        const int dim = 32 * nb + jl;
+      for (int i = 0; i < 8; ++i)
+        vf[i] = *(const u32x4*)(vt + vt_unit_off(32 * (i >> 1) + jl, 2 * (2 * kb + (i & 1)) + hh));
 #pragma unroll
-        for (int m = 0; m < 2; ++m)
-          O[nb] = Mfma<F16T>::run(*(const u32x4*)(vt + vt_unit_off(dim, 2 * (2 * kb + m) + hh)), pb[m],
-                                  O[nb]);
-      }
+      for (int i = 0; i < 8; ++i) O[i >> 1] = Mfma<F16T>::run(vf[i], pb[i & 1], O[i >> 1]);
     }
     uw0 = nw0;
     uw1 = nw1;
