@@ -311,8 +311,13 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
   // the index builder reads only LDS
   __shared__ uint16_t runCumLo[TA_CK + 1], runRowLo[TA_CK];
   __shared__ uint8_t runCumHi[TA_CK + 1], runRowHi[TA_CK];
-  __shared__ int sIdx[2][TA_KT];
-  __shared__ int sIdxK[KG ? 2 : 1][KG ? TA_KT : 1];  // MODE 2: K source rows (original order)
+  // byte offsets of each tile position's K and V source rows from the head
+  // base (built once per tile by the index wave, so the DMA issue is one add
+  // per row): sIdx for the cluster-ordered kp / vp rows (256 bytes each),
+  // sIdxK / sIdxV for rows read in place through kperm (MODE >= 2 / 3)
+  __shared__ uint32_t sIdx[2][TA_KT];
+  __shared__ uint32_t sIdxK[KG ? 2 : 1][KG ? TA_KT : 1];
+  __shared__ uint32_t sIdxV[VG ? 2 : 1][VG ? TA_KT : 1];
   __shared__ int bMark[TA_KT];
   __shared__ int wsc[TA_WAVES], wsr[TA_WAVES];
   const int total = H * maxT;
@@ -478,8 +483,9 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     // marks the tile slot where that run starts; a prefix max over the marks
     // gives each position its run.
     int r0 = 0;
-    // MODE 2: the K rows of the tile last built, loaded from kperm by the
-    // index wave and stored to sIdxK after the next wait on the memory counter
+    // MODE >= 2: the K rows of the tile last built, loaded from kperm by the
+    // index wave and stored (as byte offsets) to sIdxK / sIdxV after the next
+    // wait on the memory counter
     int kpend = 0;
     const int32_t* kph = KG ? kperm + (size_t)h * N : nullptr;
     auto build_idx = [&](int tile) {
@@ -500,7 +506,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
         const int pos = base + lane;
         const int ck = __shfl(cs, k, 64), rk = __shfl(rw, k, 64);
         const int vrow = pos < kvlen ? rk + pos - ck : 0;
-        sIdx[tile & 1][lane] = vrow;
+        sIdx[tile & 1][lane] = (uint32_t)vrow << 8;
         if constexpr (KG) kpend = pos < kvlen ? kph[vrow] : 0;
         // run holding the next tile's first position: the last run starting at
         // or before it.  The lanes see runs r0 .. r0 + 63 only; when all of
@@ -514,7 +520,10 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     };
     auto flush_k = [&](int tile) {
       if constexpr (KG)
-        if (wave == TA_WAVES - 1) sIdxK[tile & 1][lane] = kpend;
+        if (wave == TA_WAVES - 1) {
+          sIdxK[tile & 1][lane] = (uint32_t)kpend * krow_bytes;
+          if constexpr (VG) sIdxV[tile & 1][lane] = (uint32_t)kpend * vrow_bytes;
+        }
     };
     // K and V tiles via LDS DMA (each wave instruction fills 4 whole rows, the
     // lane fetching the 16-byte chunk that belongs at its swizzled position)
@@ -526,10 +535,10 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
       for (int i = 0; i < 4; ++i) {
         const int blk = 4 * i + wave;
         const int row = 4 * blk + (lane >> 4);
-        const uint32_t base = (uint32_t)sIdx[buf][row] * 256u;
-        const uint32_t kbase = KG ? (uint32_t)sIdxK[buf][row] * krow_bytes : base;
+        const uint32_t base = sIdx[buf][row];
+        const uint32_t kbase = KG ? sIdxK[buf][row] : base;
         const uint32_t offk = kbase + 16u * ((lane & 15) ^ (row & 15));
-        const uint32_t vbase = VG ? (uint32_t)sIdxK[buf][row] * vrow_bytes : base;
+        const uint32_t vbase = VG ? sIdxV[buf][row] : base;
         const uint32_t offv = vbase + 16u * ((lane & 15) ^ sv_swz(row));
         __builtin_amdgcn_global_load_lds((const glb_void_t*)(kh + offk),
                                          (lds_void_t*)(sKb + blk * 4 * 128), 16, 0, 0);
