@@ -149,7 +149,8 @@ int t2t_score_select_packed(const void* QU, const void* cks, const int32_t* kcou
  * query-cluster offsets) is a static device array of
  * T2T_NOALLOC_SCRATCH_INTS entries per GPU, held until the process ends, and
  * sizes beyond it return T2T_ERR_UNSUPPORTED.  It calls no allocator.  Calls
- * that overlap on one GPU share that array and race.  Results are
+ * that overlap on one GPU share that array and race.  The stream must belong
+ * to the current device (else T2T_ERR_UNSUPPORTED).  Results are
  * bit-identical to t2t_score_select_packed. */
 #define T2T_NOALLOC_SCRATCH_INTS 262208   /* 64 heads x (4096 + 1) */
 size_t t2t_score_select_noalloc_max_ints(void);

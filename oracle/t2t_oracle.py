@@ -143,7 +143,8 @@ def scale_centroids(ck2, scale=1.0 / math.sqrt(HEAD_DIM)):
     """state['ck'] = fp16(ck2); cks = fp16(fp32(ck2 * fp32(scale))).
 
     deploy_step.py:389,393 (torch multiplies an fp32 tensor by a Python
-    scalar in fp32, then casts to fp16).
+    scalar in fp32, then casts to fp16).  Pinned bit for bit against torch-CPU
+    in tests/test_oracle_init.py.
     """
     ck2 = np.asarray(ck2, dtype=np.float32)
     ck16 = ck2.astype(np.float16)
@@ -220,8 +221,9 @@ def q_centroid_update(x, labels, old):
         np.add.at(S, labels[h], xi[h])
         n = np.bincount(labels[h], minlength=C)[:C]
         counts[h] = n
-        mean = S.astype(np.float32) / (np.float32(32768.0) * n.astype(np.float32))[:, None]
-        mean = mean.astype(np.float32).astype(np.float16)
+        with np.errstate(invalid="ignore", divide="ignore"):    # empty clusters: replaced below
+            mean = S.astype(np.float32) / (np.float32(32768.0) * n.astype(np.float32))[:, None]
+            mean = mean.astype(np.float32).astype(np.float16)
         out[h] = np.where((n > 0)[:, None], mean, old[h])
     return out, counts
 
@@ -367,7 +369,8 @@ def select_union(gl, kcounts, qperm, qcounts, ns):
 def or_pin_tail(unip, C=C_KEYS):
     """Every query cluster executes the reserved last key cluster.
 
-    deploy_step.py:444-448.
+    deploy_step.py:444-448.  Pinned in tests/test_oracle_init.py against the
+    reference's byte-view formula and the one-bit-changed invariant.
     """
     out = unip.copy().view(np.uint32)
     out[..., (C - 1) >> 5] |= np.uint32(1) << np.uint32((C - 1) & 31)
@@ -487,7 +490,8 @@ def fast_assign(x, c):
     fast_assign.py:16-106.  The reference packs the cluster index into the
     low mantissa bits of the fp32 distance; the oracle uses the exact
     distance, so labels agree except where two distances are within the
-    packing resolution.
+    packing resolution.  Pinned against an exact-rational brute-force argmin
+    with duplicated centroids (tests/test_oracle_init.py).
     """
     xx = np.asarray(x, dtype=np.float16).astype(np.float64)
     cc = np.asarray(c, dtype=np.float16).astype(np.float64)
@@ -500,7 +504,9 @@ def det_centroid_update(x, labels, old):
 
     integrations/sglang/backend/t2t_attn.py:242-257 (_det_centroid_update):
     xi = round_half_even(x * 2^20); cent = (sum / 2^20) / n in fp64, cast to
-    fp16 through fp32 (torch's double -> half conversion).
+    fp16 through fp32 (torch's double -> half conversion).  Pinned bit for bit
+    against exact rational sums and torch-CPU's cast, with constructed
+    rounding cases (tests/test_oracle_init.py).
     Returns (new fp16 [H, C, D], counts int32 [H, C]).
     """
     x = np.asarray(x, dtype=np.float16)

@@ -128,6 +128,10 @@ def test_rocm_patch_applies_and_calls_existing_hooks(tmp_path):
     subprocess.run(["git", "-C", str(tmp_path), "apply", str(patch)], check=True)
     iface = (tmp_path / "python/sglang/multimodal_gen/runtime/platforms/interface.py").read_text()
     assert "    T2T_ATTN = enum.auto()" in iface
+    sargs = (tmp_path / "python/sglang/multimodal_gen/runtime/server_args/server_args.py").read_text()
+    # any config that is not already an addict.Dict (None included) is wrapped
+    assert "        elif not isinstance(self.attention_backend_config, addict.Dict):" in sargs
+    assert "            self.attention_backend_config = addict.Dict(self.attention_backend_config)" in sargs
     assert getattr(B.T2TAttentionBackend.get_enum(), "name", "T2T_ATTN") == "T2T_ATTN"
     assert B.AttentionBackendEnum.T2T_ATTN is B.T2TAttentionBackend.get_enum()
     called = set(re.findall(r"from token2tile_amd\.backend\.sglang_hooks import (\w+)", text))

@@ -772,12 +772,25 @@ static __device__ __align__(256) int32_t scratch[T2T_NOALLOC_SCRATCH_INTS];
 static std::mutex g_scratch_mu;
 static int32_t* g_scratch_ptr[T2T_MAX_DEVICES];
 
-static int noalloc_scratch(int32_t** out) {
+static int noalloc_scratch(hipStream_t stream, int32_t** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) {
     t2t_set_error("score_select_noalloc: hipGetDevice: %s", hipGetErrorString(e));
     return T2T_ERR_LAUNCH;
+  }
+  // The scratch address is per device: a stream of another GPU would receive
+  // a pointer into this GPU's copy of the array.
+  hipDevice_t sdev = -1;
+  e = hipStreamGetDevice(stream, &sdev);
+  if (e != hipSuccess) {
+    t2t_set_error("score_select_noalloc: hipStreamGetDevice: %s", hipGetErrorString(e));
+    return T2T_ERR_LAUNCH;
+  }
+  if ((int)sdev != dev) {
+    t2t_set_error("score_select_noalloc: stream belongs to device %d, current device is %d",
+                  (int)sdev, dev);
+    return T2T_ERR_UNSUPPORTED;
   }
   if (dev < 0 || dev >= T2T_MAX_DEVICES) {
     t2t_set_error("score_select_noalloc: device %d outside [0, %d)", dev, T2T_MAX_DEVICES);
@@ -815,7 +828,7 @@ extern "C" int t2t_score_select_packed_noalloc(const void* QU, const void* cks,
     return T2T_ERR_UNSUPPORTED;
   }
   int32_t* off = nullptr;
-  int rc = noalloc_scratch(&off);
+  int rc = noalloc_scratch((hipStream_t)stream, &off);
   if (rc) return rc;
   return score_select_launch(QU, cks, kcounts, qperm, qcounts, ns_dev, unip, rowcnt, H, N, CQ, off,
                              (hipStream_t)stream);

@@ -39,13 +39,26 @@ __all__ = ["MaskedStepDeploy", "online_u", "fast_assign", "fast_gather", "fused_
 # ---------------------------------------------------------------------------
 
 def _eigh_robust(M):
-    """Symmetric eigendecomposition; on a solver failure, retry on the host
-    LAPACK like the reference (deploy_step.py:104-111)."""
+    """Batched symmetric eigendecomposition on M's device.  The device solver
+    can fail to converge on nearly singular Grams, where the host LAPACK
+    succeeds, so a failure is retried once on the host (the reference falls
+    back the same way, deploy_step.py:104-111)."""
+    if M.device.type == "cpu":
+        return torch.linalg.eigh(M)
     try:
         return torch.linalg.eigh(M)
-    except torch._C._LinAlgError:
-        e, V = torch.linalg.eigh(M.cpu())
-        return e.to(M.device), V.to(M.device)
+    except RuntimeError:                    # torch.linalg.LinAlgError derives from it
+        return tuple(t.to(M.device) for t in torch.linalg.eigh(M.cpu()))
+
+
+def _require_finite(**tensors):
+    """Raise RuntimeError naming the heads of any input holding inf / NaN."""
+    for name, t in tensors.items():
+        per_head = torch.isfinite(t).logical_not_().flatten(1).sum(1)
+        if bool(per_head.any()):
+            heads = per_head.nonzero().flatten().tolist()
+            raise RuntimeError(f"online_u: {name} {tuple(t.shape)} holds "
+                               f"{int(per_head.sum())} non-finite values, in heads {heads}")
 
 
 def online_u(qf, kf, r=32):
@@ -60,12 +73,7 @@ def online_u(qf, kf, r=32):
     symmetric eigensolver is two orders of magnitude faster here than a
     batched SVD.  Raises RuntimeError on non-finite input.
     """
-    for name, t in (("q", qf), ("k", kf)):
-        bad = ~torch.isfinite(t)
-        if bool(bad.any()):
-            raise RuntimeError(
-                f"online_u: non-finite {name} input; per-head counts "
-                f"{bad.sum(dim=(1, 2)).tolist()}, shape {tuple(t.shape)}")
+    _require_finite(q=qf, k=kf)
 
     def gram(x):
         if x.dtype in (torch.float16, torch.bfloat16):
@@ -108,6 +116,12 @@ def fused_update_vstats(ku, labels, old_centroids, v=None, *, BLOCK_N=32, num_wa
     dtype of ku / v unless ``return_fp32``.  ``BLOCK_N`` and ``num_warps``
     are the reference's Triton tuning knobs: accepted and ignored."""
     del BLOCK_N, num_warps
+    if ku.dim() != 3 or ku.shape[2] != 32:
+        raise ValueError(f"fused_update_vstats: ku must be [H, N, 32] (the rank-32 space the "
+                         f"HIP kernel is built for), got {tuple(ku.shape)}")
+    if v is not None and (v.dim() != 3 or v.shape[2] != 128 or v.shape[:2] != ku.shape[:2]):
+        raise ValueError(f"fused_update_vstats: v must be [H, N, 128] beside ku "
+                         f"{tuple(ku.shape)}, got {tuple(v.shape)}")
     cent, counts, vmean = ops.fused_update_vstats(
         ku.contiguous(), labels.to(torch.int32).contiguous(), old_centroids.contiguous(),
         None if v is None else v.contiguous())
