@@ -14,7 +14,12 @@ Also measured: dense bf16 attention on the same GPU (this library's tile
 kernel with an all-ones union, and torch SDPA), the time of a dense call
 at the bf16 MFMA peak, init_state cold (first call of the process) and
 warm, the roofline fraction of the tile-attention kernel, and the CPU
-oracle on the CPU plumbing config on one host thread.
+oracle on the CPU plumbing config over the host cores (at most 16).
+
+A second leg (``profile_max_budget``) re-times the call at the largest
+budget the reference's built-in profile for the shape issues (720p: 4880
+tokens in the first step window), with its mean union length and the exact
+kernel's roofline fraction.
 
 Prints one JSON line.  Usage: python bench.py [--steps K] [--warmup W]
 """
@@ -31,6 +36,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# the reference's built-in budget profile for each benchmark shape
+# (integrations/sglang/backend/t2t_attn.py:95-130)
+PROFILE_FOR = {"wan720p": "wan21_t2v_14b_n75600_t50", "wan480p": "wan21_t2v_n32760_t50"}
 HBM_PEAK_GBS = 8000.0
 
 
@@ -67,10 +75,12 @@ def traffic_bytes(config, dtype):
 
 def cpu_baseline():
     """The CPU oracle (numpy restatement of the reference semantics) timed
-    on one full call of the CPU plumbing config, on one host thread (the
-    BLAS pool is limited to one thread; the rest is single-threaded numpy)."""
+    on one structure-rebuilding call of the CPU plumbing config, with its
+    row-parallel stages spread over the host cores this process may use
+    (at most 16, the box's CPU share for one GPU), one BLAS thread each."""
     import numpy as np
     from threadpoolctl import threadpool_limits
+    from oracle import parallel as P
     from oracle import t2t_oracle as O
     from token2tile_amd.synth import CONFIGS, budget, generate_np
     H, N, grid, frac, CQ = CONFIGS["cpu_plumbing"]
@@ -81,16 +91,19 @@ def cpu_baseline():
     rng = np.random.default_rng(0)
     st = dict(Uq=Uq, Uk=Uk, ck=KU[:, np.sort(rng.choice(N, 2048, replace=False))],
               cq=QU[:, np.sort(rng.choice(N, CQ, replace=False))])
-    calls = 2
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    calls = 3
     with threadpool_limits(limits=1):
+        P.full_call_pool(q, k, v, st, budget(N, frac), CQ, workers=cores)   # warm-up
         t0 = time.perf_counter()
         for _ in range(calls):
-            O.full_call(q, k, v, st, budget(N, frac), CQ)
+            P.full_call_pool(q, k, v, st, budget(N, frac), CQ, workers=cores)
         dt = (time.perf_counter() - t0) / calls
-    return {"value": round(dt * 1e3, 1), "unit": "ms/call", "cores": 1, "kind": "port",
+    return {"value": round(dt * 1e3, 1), "unit": "ms/call", "cores": cores, "kind": "port",
             "sample": f"mean of {calls} structure-rebuilding calls of the numpy oracle on the CPU "
                       f"plumbing config (H={H}, N={N}, CQ={CQ}, ns={budget(N, frac)}, fp32/fp64), "
-                      f"one host thread"}
+                      f"selection, exact attention and merge split over {cores} processes "
+                      f"(host cores available: {os.cpu_count()}), one BLAS thread each"}
 
 
 def main():
@@ -142,46 +155,55 @@ def main():
         deploy.stage_events = None
         return out
 
-    for _ in range(args.warmup):
-        one_step()
-    torch.cuda.synchronize()
-    # timed region: exactly K steps.  Stage events are recorded on the
-    # operator's own stream (s_main), where every stage kernel is launched.
-    records = []
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        ev = []
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record()
-        one_step(ev)
-        b.record()
-        records.append((deploy.last_call_full, a, b, ev))
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    print(f"[bench] {args.steps} steps: {wall_ms:.3f} ms/step", file=sys.stderr, flush=True)
+    def timed(steps, warmup):
+        """warm-up, then exactly `steps` timed steps; returns ms/step, the
+        full / reuse call means and the per-stage means (HIP events on the
+        operator's stream, s_main, where every stage kernel is launched)."""
+        for _ in range(warmup):
+            one_step()
+        torch.cuda.synchronize()
+        records = []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            ev = []
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            one_step(ev)
+            b.record()
+            records.append((deploy.last_call_full, a, b, ev))
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / steps
+        stages = {"full": {}, "reuse": {}}
+        calls = {"full": [], "reuse": []}
+        kern = {"attention_exact": [], "attention_residual": []}
+        for full, a, b, ev in records:
+            kind = "full" if full else "reuse"
+            calls[kind].append(a.elapsed_time(b))
+            for name, e0, e1 in ev:
+                ms = e0.elapsed_time(e1)
+                stages[kind].setdefault(name, []).append(ms)
+                if name in kern:
+                    kern[name].append(ms)
+        st_ms = {kd: {n: round(sum(x) / len(x), 4) for n, x in d.items()} for kd, d in stages.items()}
+        mean = lambda x: sum(x) / max(1, len(x))
+        return wall, mean(calls["full"]), mean(calls["reuse"]), st_ms, {n: mean(x) for n, x in kern.items()}
 
-    stages = {"full": {}, "reuse": {}}
-    call_ms = {"full": [], "reuse": []}
-    kern_ms = {"attention_exact": [], "attention_residual": []}
-    for full, a, b, ev in records:
-        kind = "full" if full else "reuse"
-        call_ms[kind].append(a.elapsed_time(b))
-        for name, e0, e1 in ev:
-            ms = e0.elapsed_time(e1)
-            stages[kind].setdefault(name, []).append(ms)
-            if name in kern_ms:
-                kern_ms[name].append(ms)
-    stage_ms = {kd: {n: round(sum(x) / len(x), 4) for n, x in d.items()} for kd, d in stages.items()}
-    full_ms = sum(call_ms["full"]) / max(1, len(call_ms["full"]))
-    reuse_ms = sum(call_ms["reuse"]) / max(1, len(call_ms["reuse"]))
+    def kv_rows():
+        snap = deploy._cfg_hold[0]
+        pv = ops.plan_views(snap["tile_attn_plan"], H, N, CQ)
+        return (pv["kvlen"].long() * snap["tile_sizes"].long()).sum().item()
+
+    wall_ms, full_ms, reuse_ms, stage_ms, kmean = timed(args.steps, args.warmup)
+    print(f"[bench] {args.steps} steps: {wall_ms:.3f} ms/step", file=sys.stderr, flush=True)
     print(f"[bench] full {full_ms:.3f} ms, reuse {reuse_ms:.3f} ms, stages {stage_ms}",
           file=sys.stderr, flush=True)
+    kern_ms = {"attention_exact": [kmean["attention_exact"]],
+               "attention_residual": [kmean["attention_residual"]]}
 
     # executed attention work: 4 * D * sum_t rows_t * kv_len_t
     snap = deploy._cfg_hold[0]
-    pv = ops.plan_views(snap["tile_attn_plan"], H, N, CQ)
-    rows_kv = (pv["kvlen"].long() * snap["tile_sizes"].long()).sum().item()
+    rows_kv = kv_rows()
     attn_flops = 4.0 * 128 * rows_kv
     tail_flops = 2.0 * H * N * 2048 * (32 + 128)
     dense_flops = 4.0 * H * N * N * 128
@@ -192,6 +214,28 @@ def main():
     attn_tflops = attn_flops / (attn_ms * 1e-3) / 1e12
     tail_tflops = tail_flops / (tail_ms * 1e-3) / 1e12
     value = wall_ms
+
+    # second leg: the largest budget the reference's built-in profile for this
+    # shape issues (its first step window), where the exact attention carries
+    # most of an end-to-end denoising step
+    peak_leg = None
+    prof = PROFILE_FOR.get(args.config)
+    if prof is not None and args.steps >= 4:
+        from token2tile_amd.backend import t2t_attn as BK
+        ns_peak = max(BK._ns_map(BK._WAN_PROFILES[prof], N).values())
+        deploy.ns_t.fill_(ns_peak)
+        w2, f2, r2, st2, k2 = timed(8, 4)
+        rk2 = kv_rows()
+        fl2 = 4.0 * 128 * rk2
+        peak_leg = {"profile": prof, "budget_tokens": ns_peak, "ms_per_step": round(w2, 4),
+                    "full_call_ms": round(f2, 3), "reuse_call_ms": round(r2, 3),
+                    "mean_kv_len": round(rk2 / (H * N), 1), "stage_ms": st2,
+                    "attn_kernel_ms": round(k2["attention_exact"], 4),
+                    "attn_frac": round(fl2 / (k2["attention_exact"] * 1e-3) / 1e12
+                                       / MFMA_BF16_PEAK_TFLOPS, 4),
+                    "residual_kernel_ms": round(k2["attention_residual"], 4)}
+        print(f"[bench] profile max budget {ns_peak}: {peak_leg}", file=sys.stderr, flush=True)
+        deploy.ns_t.fill_(budget(N, frac))
 
     result_dense = {}
     if not args.no_dense:
@@ -276,6 +320,7 @@ def main():
                               "frac": round(tail_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                               "kernel_ms": round(tail_ms, 4)},
         "cpu_baseline": cpu,
+        "profile_max_budget": peak_leg,
     }
     print(json.dumps(out), flush=True)
 

@@ -394,7 +394,8 @@ def kv_rows_of_union(uni_row, k_off):
     return np.concatenate([np.arange(k_off[c], k_off[c + 1]) for c in cl])
 
 
-def tile_attention(q, kp, vp, qcounts, kcounts, unip, qperm, scale=1.0 / math.sqrt(HEAD_DIM)):
+def tile_attention(q, kp, vp, qcounts, kcounts, unip, qperm, scale=1.0 / math.sqrt(HEAD_DIM),
+                   heads=None, clusters=None):
     """Exact attention of every sorted query over its cluster's union.
 
     tile_attn/src/kernel.cu:820-1096 (attn_kernel): query j of the sorted
@@ -404,18 +405,21 @@ def tile_attention(q, kp, vp, qcounts, kcounts, unip, qperm, scale=1.0 / math.sq
     Computed in fp64.  Pinned by: an all-ones union equals dense attention
     (torch SDPA) and a single-cluster union equals a hand-sliced softmax.
     Returns (out fp64 [H, N, D] sorted order, lse fp64 [H, N]).
+    ``heads`` / ``clusters`` restrict the work to those heads and query
+    clusters (the other rows stay 0 / -inf), so a caller can split one call
+    over processes.
     """
     H, N, D = q.shape
     CQ = qcounts.shape[1]
     out = np.zeros((H, N, D), dtype=np.float64)
     lse = np.full((H, N), -np.inf, dtype=np.float64)
     uni = unpack_bits(unip)
-    for h in range(H):
+    for h in (range(H) if heads is None else heads):
         k_off = np.concatenate([[0], np.cumsum(kcounts[h])])
         qoff = exclusive_scan(qcounts[h])
         kh = kp[h].astype(np.float64)
         vh = vp[h].astype(np.float64)
-        for t in range(CQ):
+        for t in (range(CQ) if clusters is None else clusters):
             n = int(qcounts[h, t])
             if n == 0:
                 continue
@@ -437,7 +441,8 @@ def tile_attention(q, kp, vp, qcounts, kcounts, unip, qperm, scale=1.0 / math.sq
 # S6: centroid residual over the unselected clusters, and the merge
 # ---------------------------------------------------------------------------
 
-def tail_merge(attn_out, attn_lse, QU, cks, sumv, kcounts, unip, qlab, qperm, lam, tailw=1.0):
+def tail_merge(attn_out, attn_lse, QU, cks, sumv, kcounts, unip, qlab, qperm, lam, tailw=1.0,
+               heads=None, rows=None):
     """Per-query residual over the clusters outside its union, merged under
     one softmax with the exact part; written at the original row.
 
@@ -450,23 +455,25 @@ def tail_merge(attn_out, attn_lse, QU, cks, sumv, kcounts, unip, qlab, qperm, la
     result is shift invariant); the oracle uses max_c s_c + 2 like the
     reference.  Pinned by closed forms: empty union -> lam*O/phi; full union
     -> exact output; tw = 0 -> exact output (tests/test_oracle_attention.py).
+    ``heads`` / ``rows`` (a slice of sorted positions) restrict the work; the
+    other rows of the result stay 0.
     """
     H, N, D = attn_out.shape
     out = np.zeros((H, N, D), dtype=np.float64)
     uni = unpack_bits(unip)
-    for h in range(H):
-        s_all = scores(QU[h][None], cks[h][None])[0].astype(np.float64)   # [N orig, C]
+    sl = slice(None) if rows is None else rows
+    for h in (range(H) if heads is None else heads):
         cnt = kcounts[h].astype(np.float64)
         sv = sumv[h].astype(np.float64)
-        orig = qperm[h]
-        s = s_all[orig]                                    # sorted order
+        orig = qperm[h][sl]
+        s = scores(QU[h][orig][None], cks[h][None])[0].astype(np.float64)   # sorted order
         mask = uni[h][qlab[h][orig]]                       # in-union clusters
         m = s.max(axis=1) + 2.0
         p = np.where(mask, 0.0, np.exp(s - m[:, None]))
         phi = p @ cnt
         p16 = p.astype(np.float32).astype(np.float16).astype(np.float64)
         O = p16 @ sv
-        le = attn_lse[h] * LN2
+        le = attn_lse[h][sl] * LN2
         M = np.maximum(le, m)
         with np.errstate(invalid="ignore"):
             ex = np.exp(le - M)
@@ -474,8 +481,9 @@ def tail_merge(attn_out, attn_lse, QU, cks, sumv, kcounts, unip, qlab, qperm, la
         ph = st * phi
         bad = ph <= 1e-6 * ex
         den = np.maximum(ex + ph * tailw, 1e-12)
-        merged = (ex / den)[:, None] * attn_out[h] + (st * tailw * lam[h] / den)[:, None] * O
-        res = np.where(bad[:, None], attn_out[h], merged)
+        ao = attn_out[h][sl]
+        merged = (ex / den)[:, None] * ao + (st * tailw * lam[h] / den)[:, None] * O
+        res = np.where(bad[:, None], ao, merged)
         out[h, orig] = res
     return out
 
