@@ -260,54 +260,29 @@ __global__ __launch_bounds__(256) void sort_hist_kernel(const int32_t* __restric
   for (int i = tid; i < C; i += 256) out[i] = hist[i];
 }
 
-__global__ __launch_bounds__(1024) void sort_scan_kernel(int32_t* __restrict__ chist,
-                                                         int32_t* __restrict__ counts,
-                                                         int32_t* __restrict__ cbase, int C,
-                                                         int nChunk) {
-  __shared__ int wsum[16];
-  __shared__ int sbase[KM_MAXC];
-  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  int32_t* ch = chist + (size_t)h * nChunk * C;
-  // column scans over chunks: chunk-local start offsets, and totals
-  for (int c = tid; c < C; c += 1024) {
-    int run = 0;
-    for (int k = 0; k < nChunk; ++k) {
-      const int v = ch[(size_t)k * C + c];
-      ch[(size_t)k * C + c] = run;
-      run += v;
-    }
-    sbase[c] = run;
-    counts[(size_t)h * C + c] = run;
-  }
-  __syncthreads();
-  // exclusive scan of the totals over clusters (4 per thread, in order)
-  const int per = (C + 1023) / 1024;
-  int loc = 0;
-  for (int i = 0; i < per; ++i) {
-    const int c = tid * per + i;
-    if (c < C) loc += sbase[c];
-  }
-  const int inc = wave_incl_scan(loc);
-  if (lane == 63) wsum[w] = inc;
-  __syncthreads();
-  int add = 0;
-  for (int i = 0; i < w; ++i) add += wsum[i];
-  int run = add + inc - loc;
-  __syncthreads();
-  for (int i = 0; i < per; ++i) {
-    const int c = tid * per + i;
-    if (c < C) {
-      const int v = sbase[c];
-      sbase[c] = run;
-      run += v;
+// chunk-local start offsets: chist[h, k, c] <- sum of chist[h, k', c] over
+// k' < k, and counts[h, c] <- the column total.  One wave per 64 clusters,
+// lane = cluster; the chunks are read 16 at a time (all in flight together),
+// so the latency is a few memory round trips, not one per chunk.
+#define SCAN_GRP 16
+__global__ __launch_bounds__(64) void sort_colscan_kernel(int32_t* __restrict__ chist,
+                                                          int32_t* __restrict__ counts, int C,
+                                                          int nChunk) {
+  const int h = blockIdx.y, c = blockIdx.x * 64 + threadIdx.x;
+  if (c >= C) return;
+  int32_t* col = chist + (size_t)h * nChunk * C + c;
+  int run = 0;
+  for (int k0 = 0; k0 < nChunk; k0 += SCAN_GRP) {
+    int v[SCAN_GRP];
+#pragma unroll
+    for (int i = 0; i < SCAN_GRP; ++i) v[i] = k0 + i < nChunk ? col[(size_t)(k0 + i) * C] : 0;
+#pragma unroll
+    for (int i = 0; i < SCAN_GRP; ++i) {
+      if (k0 + i < nChunk) col[(size_t)(k0 + i) * C] = run;
+      run += v[i];
     }
   }
-  __syncthreads();
-  for (int c = tid; c < C; c += 1024) {
-    const int b = sbase[c];
-    cbase[(size_t)h * C + c] = b;
-    for (int k = 0; k < nChunk; ++k) ch[(size_t)k * C + c] += b;
-  }
+  counts[(size_t)h * C + c] = run;
 }
 
 __device__ inline void wave_sync_km() {
@@ -315,23 +290,38 @@ __device__ inline void wave_sync_km() {
   __builtin_amdgcn_wave_barrier();
 }
 
-// one wave per chunk; rows of equal label keep their order (ballot ranking)
+// One wave per chunk of SORT_CH rows; rows of equal label keep their order
+// (ballot ranking).  A cluster's start in the permutation is cbase (the
+// exclusive scan of the counts over clusters) plus the chunk-local offset.
+// The chunk's labels are loaded up front, so the ranking loop waits on no
+// global load.
+#define SC_PER (SORT_CH / 64)
 __global__ __launch_bounds__(64) void sort_scatter_kernel(const int32_t* __restrict__ lab,
                                                           const int32_t* __restrict__ chist,
+                                                          const int32_t* __restrict__ cbase,
                                                           int32_t* __restrict__ perm, int N, int C,
                                                           int nChunk, int lbits) {
-  __shared__ int cc[KM_MAXC];
+  extern __shared__ int cc[];  // C entries
   const int h = blockIdx.y, k = blockIdx.x, l = threadIdx.x;
-  const int32_t* off = chist + ((size_t)h * nChunk + k) * C;
-  for (int i = l; i < C; i += 64) cc[i] = off[i];
-  wave_sync_km();
   const int r0 = k * SORT_CH;
   const int r1 = (r0 + SORT_CH) < N ? (r0 + SORT_CH) : N;
+  int labs[SC_PER];
+#pragma unroll
+  for (int i = 0; i < SC_PER; ++i) {
+    const int row = r0 + 64 * i + l;
+    labs[i] = row < r1 ? lab[(size_t)h * N + row] : 0;
+  }
+  const int32_t* off = chist + ((size_t)h * nChunk + k) * C;
+  const int32_t* cb = cbase + (size_t)h * C;
+  for (int c = l; c < C; c += 64) cc[c] = cb[c] + off[c];
+  wave_sync_km();
   const unsigned long long lt = (1ull << l) - 1ull;
-  for (int r = r0; r < r1; r += 64) {
-    const int row = r + l;
+#pragma unroll
+  for (int i = 0; i < SC_PER; ++i) {
+    const int row = r0 + 64 * i + l;
+    if (r0 + 64 * i >= r1) break;  // wave-uniform
     const bool valid = row < r1;
-    const int c = valid ? lab[(size_t)h * N + row] : 0;
+    const int c = labs[i];
     unsigned long long peers = __ballot(valid);
     for (int b = 0; b < lbits; ++b) {
       const unsigned long long bb = __ballot((c >> b) & 1);
@@ -350,6 +340,31 @@ __global__ __launch_bounds__(64) void sort_scatter_kernel(const int32_t* __restr
   }
 }
 
+// cbase[h, c] = exclusive scan of counts[h, :] over clusters
+__global__ __launch_bounds__(1024) void cbase_kernel(const int32_t* __restrict__ counts,
+                                                     int32_t* __restrict__ cbase, int C) {
+  __shared__ int wsum[16];
+  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int per = (C + 1023) / 1024;
+  int loc = 0;
+  for (int i = 0; i < per; ++i) {
+    const int c = tid * per + i;
+    if (c < C) loc += counts[(size_t)h * C + c];
+  }
+  const int inc = wave_incl_scan(loc);
+  if (lane == 63) wsum[w] = inc;
+  __syncthreads();
+  int run = inc - loc;
+  for (int i = 0; i < w; ++i) run += wsum[i];
+  for (int i = 0; i < per; ++i) {
+    const int c = tid * per + i;
+    if (c < C) {
+      cbase[(size_t)h * C + c] = run;
+      run += counts[(size_t)h * C + c];
+    }
+  }
+}
+
 struct SortBufs {
   int32_t* chist;  // [H, nChunk, C]
 };
@@ -360,9 +375,11 @@ static int run_sort(const int32_t* lab, int32_t* counts, int32_t* cbase, int32_t
   int lbits = 1;
   while ((1 << lbits) < C) ++lbits;
   hipLaunchKernelGGL(sort_hist_kernel, dim3(nChunk, H), dim3(256), 0, st, lab, chist, N, C, nChunk);
-  hipLaunchKernelGGL(sort_scan_kernel, dim3(H), dim3(1024), 0, st, chist, counts, cbase, C, nChunk);
-  hipLaunchKernelGGL(sort_scatter_kernel, dim3(nChunk, H), dim3(64), 0, st, lab, chist, perm, N, C,
-                     nChunk, lbits);
+  hipLaunchKernelGGL(sort_colscan_kernel, dim3(cdiv(C, 64), H), dim3(64), 0, st, chist, counts, C,
+                     nChunk);
+  hipLaunchKernelGGL(cbase_kernel, dim3(H), dim3(1024), 0, st, counts, cbase, C);
+  hipLaunchKernelGGL(sort_scatter_kernel, dim3(nChunk, H), dim3(64), (size_t)C * sizeof(int), st,
+                     lab, chist, cbase, perm, N, C, nChunk, lbits);
   return t2t_check_launch("counting sort");
 }
 
@@ -738,30 +755,6 @@ extern "C" int t2t_kmm_run_strided(const void* QU, const void* KU, const void* V
 }
 
 // ---- value statistics of a reuse call ----
-__global__ __launch_bounds__(1024) void cbase_kernel(const int32_t* __restrict__ counts,
-                                                     int32_t* __restrict__ cbase, int C) {
-  __shared__ int wsum[16];
-  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int per = (C + 1023) / 1024;
-  int loc = 0;
-  for (int i = 0; i < per; ++i) {
-    const int c = tid * per + i;
-    if (c < C) loc += counts[(size_t)h * C + c];
-  }
-  const int inc = wave_incl_scan(loc);
-  if (lane == 63) wsum[w] = inc;
-  __syncthreads();
-  int run = inc - loc;
-  for (int i = 0; i < w; ++i) run += wsum[i];
-  for (int i = 0; i < per; ++i) {
-    const int c = tid * per + i;
-    if (c < C) {
-      cbase[(size_t)h * C + c] = run;
-      run += counts[(size_t)h * C + c];
-    }
-  }
-}
-
 struct VWs {
   int32_t* cbase;
   float* vsum;
