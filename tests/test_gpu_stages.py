@@ -180,7 +180,15 @@ def test_select_union_bit_exact(dev, kind, ns):
 # alternating_scale: consecutive rows (in the order the kernels walk them)
 # differ in score scale by 2500x, so the lower bound carried over from the
 # previous row is far off and the selection must fall back to a full pass
-FUSED_CASES = ["normal", "tied_centroids", "zeros", "one_per_cluster", "alternating_scale"]
+# all_tied: every centroid equal, so every score of a row ties (2048 candidates,
+# more than a row's list holds, and more tied clusters than the candidate
+# path takes: the full-row path).  coarse: centroids on a coarse grid, so a
+# few clusters tie at the crossing key (the tie path on candidates).
+# jumps: row scales that move the crossing key by a few hundred keys between
+# consecutive rows (windows above and below the predicted one) and by more
+# than the batch floor margin between batches (rows below the floor).
+FUSED_CASES = ["normal", "tied_centroids", "zeros", "one_per_cluster", "alternating_scale",
+               "all_tied", "coarse", "jumps"]
 
 
 @pytest.mark.parametrize("kind", FUSED_CASES)
@@ -195,6 +203,11 @@ def test_score_select_fused_matches_split(dev, kind, ns):
     ck2 = rng.normal(0, 0.5, (H, 2048, 32)).astype(np.float32)
     if kind == "tied_centroids":                 # duplicated centroids -> exactly tied scores
         ck2[:, 1024:] = ck2[:, :1024]
+    if kind == "all_tied":
+        ck2[:] = ck2[:, :1]
+    if kind == "coarse":
+        ck2 = (np.round(ck2 * 2) / 2).astype(np.float32)
+        QU = (np.round(QU.astype(np.float32) * 2) / 2).astype(np.float16)
     sizes = np.stack([rng.multinomial(N, np.ones(2048) / 2048) for _ in range(H)]).astype(np.int32)
     if kind == "zeros":                         # 1500 empty key clusters, same key total
         for h in range(H):
@@ -208,6 +221,11 @@ def test_score_select_fused_matches_split(dev, kind, ns):
     else:
         qlab = rng.integers(0, CQ - 1, (H, N)).astype(np.int32)   # cluster CQ-1 stays empty
     qperm, qcounts = O.stable_perm(qlab, CQ)
+    if kind == "jumps":
+        j = np.arange(N)
+        scale = (1.0 + 0.6 * np.sin(j * 0.7) + 4.0 * ((j // 64) % 3 == 1)).astype(np.float32)
+        for h in range(H):
+            QU[h, qperm[h]] = (QU[h, qperm[h]].astype(np.float32) * scale[:, None]).astype(np.float16)
     if kind == "alternating_scale":
         scale = np.where(np.arange(N) % 2 == 1, 50.0, 0.02).astype(np.float32)
         for h in range(H):
