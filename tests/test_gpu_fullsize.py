@@ -21,6 +21,10 @@ For heads 0 and H-1 of every shape:
   residual merge over the call's structure at the full key length, within
   the bf16 tolerance.
 
+The same checks run at 720p at the budgets of the reference's Wan profile
+(4880 and 4538 keys per query), on the synthetic data and on unstructured
+q/k whose unions hold most of the keys.
+
 The output is finite and bit-identical when the call is repeated.  At 720p a
 ``mask_refresh=4`` reuse call (3 of every 4 calls of the benchmark schedule)
 with a new V and a perturbed Q is checked the same way against the oracle's
@@ -160,13 +164,9 @@ def check_sampled_attention(op, q, k, out, vp_h, sumv_h, lam_h, h, rng, dev, wha
     assert cos(got, eo) >= 0.999
 
 
-@pytest.mark.parametrize("name,dtype", SHAPES, ids=[f"{n}-{str(d)[6:]}" for n, d in SHAPES])
-def test_full_size_call(dev, name, dtype):
-    from token2tile_amd import ops, synth
+def _check_full_call(dev, name, H, N, CQ, frac, q, k, v):
+    from token2tile_amd import ops
     from token2tile_amd.deploy_step import MaskedStepDeploy
-    H, N, grid, frac, CQ = synth.CONFIGS[name]
-    print(f"[fullsize] {name} {dtype}: H={H} N={N} CQ={CQ} frac={frac}", flush=True)
-    q, k, v = synth.generate(H, N, grid=grid, seed=11, device=dev, dtype=dtype)
     op = MaskedStepDeploy(H, N, CQ, s_frac=frac, device=dev)
     state = op.init_state(q, k, seed=3)
     st0 = {n_: t_.clone() for n_, t_ in state.items()}
@@ -178,6 +178,9 @@ def test_full_size_call(dev, name, dtype):
     assert torch.equal(out, out2)
     for n_ in ("ck", "cq"):
         assert torch.equal(state[n_], st1[n_])
+    pv = ops.plan_views(op._last["plan"], H, N, CQ)
+    kv = (pv["kvlen"].long() * op._last["tile_sizes"].long()).sum().item() / (H * N)
+    print(f"[fullsize] {name}: ns={op.ns} mean union {kv:.0f} keys ({kv / N:.3f} of N)", flush=True)
 
     rng = np.random.default_rng(7)
     for h in (0, H - 1):
@@ -188,6 +191,38 @@ def test_full_size_call(dev, name, dtype):
         vp_h = c(v[h][op._last["kperm"][h].long()].float())
         check_sampled_attention(op, q, k, out, vp_h, c(op._kmm_sumv[h]),
                                 c(op._kmm_lam[h:h + 1]), h, rng, dev, name)
+    return kv
+
+
+@pytest.mark.parametrize("name,dtype", SHAPES, ids=[f"{n}-{str(d)[6:]}" for n, d in SHAPES])
+def test_full_size_call(dev, name, dtype):
+    from token2tile_amd import synth
+    H, N, grid, frac, CQ = synth.CONFIGS[name]
+    print(f"[fullsize] {name} {dtype}: H={H} N={N} CQ={CQ} frac={frac}", flush=True)
+    q, k, v = synth.generate(H, N, grid=grid, seed=11, device=dev, dtype=dtype)
+    _check_full_call(dev, name, H, N, CQ, frac, q, k, v)
+
+
+@pytest.mark.parametrize("kind,ns", [("structured", 4880), ("unstructured", 4538)])
+def test_full_size_call_at_profile_budgets(dev, kind, ns):
+    """720p at the budgets of the reference's Wan profile (the largest, 4880
+    keys per query; 4538 in its first sparse window), on the synthetic grid
+    data and on unstructured q/k (iid normal, unit variance per element, as
+    a randomly initialised DiT's RMS-normalised q/k are): there the unions
+    hold most of the keys (runs of up to 2048 clusters, key lengths near N),
+    the regime of the end-to-end harness."""
+    from token2tile_amd import synth
+    H, N, grid, _, CQ = synth.CONFIGS["wan720p"]
+    frac = (ns + 0.5) / N
+    if kind == "structured":
+        q, k, v = synth.generate(H, N, grid=grid, seed=14, device=dev, dtype=torch.bfloat16)
+    else:
+        g = torch.Generator(device=dev).manual_seed(15)
+        q, k, v = (torch.randn(H, N, 128, generator=g, device=dev).to(torch.bfloat16)
+                   for _ in range(3))
+    kv = _check_full_call(dev, f"wan720p-{kind}-ns{ns}", H, N, CQ, frac, q, k, v)
+    if kind == "unstructured":
+        assert kv > 0.5 * N  # the long-union regime this case is for
 
 
 def test_full_size_reuse_call_720p(dev):
