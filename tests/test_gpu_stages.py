@@ -448,6 +448,60 @@ def test_tile_attention_exact(dev, dtype):
     assert np.all(got[~fin] == 0)
 
 
+def test_exact_task_forms_and_tile_counts(dev):
+    """Both task forms of the exact kernel at every tile count: query
+    clusters of 1, 2, 3 and 4 waves (tasks of <= 3 waves stage their tiles
+    from a producer wave, 4-wave tasks by all waves with a per-tile barrier),
+    each with union lengths of 0, 2, 64, 66, 128, 130, 200 and 1000 keys
+    (0, 1, 1, 2, 2, 3, 4 and 16 tiles), against the oracle, and the K/V
+    gather through kperm bit-identical to the gathered kp / vp."""
+    from token2tile_amd import ops
+    rng = np.random.default_rng(31)
+    H, N = 1, 4096
+    sizes = (20, 50, 90, 128)
+    nsel = (0, 1, 32, 33, 64, 65, 100, 500)          # key clusters of 2 rows each
+    CQ = len(sizes) * len(nsel) + 1
+    q = rng.normal(0, 1, (H, N, 128)).astype(np.float16)
+    k = rng.normal(0, 1, (H, N, 128)).astype(np.float16)
+    v = rng.normal(0, 1, (H, N, 128)).astype(np.float16)
+    klab = rng.permutation(np.arange(N) // 2).astype(np.int32)[None]
+    kperm, kcounts = O.stable_perm(klab, 2048)
+    labs, sel = [], np.zeros((H, CQ, 2048), dtype=bool)
+    t = 0
+    for sz in sizes:
+        for n in nsel:
+            labs += [t] * sz
+            sel[0, t, rng.choice(2048, n, replace=False)] = True
+            t += 1
+    labs += [t] * (N - len(labs))                    # the rest: one cluster, full union
+    sel[0, t] = True
+    qlab = rng.permutation(np.array(labs, dtype=np.int32))[None]
+    qperm, qcounts = O.stable_perm(qlab, CQ)
+    unip = O.pack_bits(sel)
+    kp = np.stack([k[h][kperm[h]] for h in range(H)])
+    vp = np.stack([v[h][kperm[h]] for h in range(H)])
+    for dtype in (torch.float16, torch.bfloat16):
+        tq, tk, tv, tkp, tvp = (g(a, dev).to(dtype) for a in (q, k, v, kp, vp))
+        plan = ops.tile_plan(g(qcounts, dev), g(kcounts, dev), g(unip, dev), N)
+        ao, lse = ops.tile_attn_exact(tq, tkp, tvp, g(kcounts, dev), g(unip, dev), g(qperm, dev),
+                                      plan)
+        qf, kpf, vpf = (c(t_.float()) for t_ in (tq, tkp, tvp))
+        eo, el = O.tile_attention(qf, kpf, vpf, qcounts, kcounts, unip, qperm)
+        got = c(ao.float())
+        tol = 4e-3 if dtype == torch.float16 else 2e-2
+        assert np.abs(got - eo).max() < tol
+        fin = np.isfinite(el)
+        assert np.array_equal(fin, np.isfinite(c(lse)))
+        assert np.abs(c(lse)[fin] - el[fin]).max() < 2e-3
+        assert np.all(got[~fin] == 0)
+        args = (g(kcounts, dev), g(unip, dev), g(qperm, dev), plan)
+        out_a, lse_a = torch.zeros_like(tq), torch.zeros(H, N, dtype=torch.float32, device=dev)
+        out_b, lse_b = torch.zeros_like(tq), torch.zeros(H, N, dtype=torch.float32, device=dev)
+        ops.tile_attn_exact_orig(tq, tkp, tvp, *args, out_a, lse_a)
+        ops.tile_attn_exact_orig_gather_kv(tq, tk, tv, g(kperm, dev), *args, out_b, lse_b)
+        assert torch.equal(out_a, out_b) and torch.equal(lse_a, lse_b)
+
+
 def test_full_union_equals_sdpa(dev):
     from token2tile_amd import ops
     rng = np.random.default_rng(10)

@@ -8,7 +8,11 @@
 //     rows through kperm, or from the cluster-ordered kp);
 //   * K and V tiles are gathered by LDS DMA into a double-buffered ring, row
 //     major with an XOR swizzle; tile t is consumed while tile t+1 is in
-//     flight, one barrier per tile;
+//     flight.  In tasks of four query waves every wave stages a quarter of
+//     each tile, one barrier per tile; in smaller tasks the last wave (which
+//     holds no queries) stages every tile and publishes it through an LDS
+//     flag, and the query waves report each buffer they finish through an LDS
+//     counter, so no wave waits for the slowest one at every tile;
 //   * S^T = K Q^T and O^T = V^T P^T on MFMA, so every lane owns one query: the
 //     online-softmax max/sum need one cross-half exchange, and the per-query
 //     rescale of O touches only the lane's own registers; the score chains
@@ -226,6 +230,7 @@ __device__ inline int xcd_remap(int bid, int total) {
   return (r / 8) * 64 + (bid % 8) * 8 + r % 8;
 }
 
+#define T2T_SPIN_CAP (1 << 20)  // polls before a producer/consumer wait gives up
 #define TA_MARGIN 3.0f   // log2 units of headroom when the exact-part max advances
 // a tile is redone with a new max when one lane's weight sum passes this: far
 // inside the range of bf16 P (fp32 exponents), below fp16's largest value
@@ -319,6 +324,13 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
   __shared__ uint32_t sIdxK[KG ? 2 : 1][KG ? TA_KT : 1];
   __shared__ uint32_t sIdxV[VG ? 2 : 1][VG ? TA_KT : 1];
   __shared__ int bMark[TA_KT];
+  // producer/consumer form (tasks whose last wave holds no queries): the tile
+  // last published in each buffer (tile + 1) and the count of consumer waves
+  // done with each buffer, both monotonic
+  // sAbort: set when a wait passes T2T_SPIN_CAP polls; every later wait of the
+  // work-group then returns at once, so a broken handshake ends the kernel
+  // (with a wrong result) instead of hanging it
+  __shared__ int sReady[2], sDone[2], sAbort;
   __shared__ int wsc[TA_WAVES], wsr[TA_WAVES];
   const int total = H * maxT;
   const int lin = xcd_remap(blockIdx.x, total);
@@ -403,14 +415,14 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
   // tile.  The reads of dim block nb + 1 are issued before the MFMAs of nb,
   // and an explicit lgkmcnt wait that names nb's fragments as its operands
   // orders those MFMAs after their data (no other LDS access is in flight).
-  auto pv = [&](f32x16 (&Oa)[4], const uint16_t* sVb, const u32x4 (&pb)[4]) {
+  auto pv = [&](f32x16 (&Oa)[4], const uint16_t* sVb, const u32x4 (&pb)[4]) __attribute__((always_inline)) {
     const uint32_t vbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)sVb;
     uint32_t ad[4];
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb)
       ad[nb] = vbase + 2u * (uint32_t)(trkey * 128 + 8 * ((4 * nb + (trdim >> 3)) ^ sv_swz(trkey)) + (trdim & 7));
     u32x2 fr[2][8];
-    auto rd8 = [&](u32x2 (&f)[8], uint32_t a) {
+    auto rd8 = [&](u32x2 (&f)[8], uint32_t a) __attribute__((always_inline)) {
       asm volatile(
           "ds_read_b64_tr_b16 %0, %8\n\t"
           "ds_read_b64_tr_b16 %1, %8 offset:2048\n\t"
@@ -447,7 +459,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  auto rescale = [&](f32x16 (&Oa)[4], float alpha) {
+  auto rescale = [&](f32x16 (&Oa)[4], float alpha) __attribute__((always_inline)) {
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
@@ -488,7 +500,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     // wait on the memory counter
     int kpend = 0;
     const int32_t* kph = KG ? kperm + (size_t)h * N : nullptr;
-    auto build_idx = [&](int tile) {
+    auto build_idx = [&](int tile) __attribute__((always_inline)) {
       if (wave == TA_WAVES - 1) {
         const int base = tile * TA_KT;
         const int r = r0 + lane;
@@ -518,7 +530,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
         r0 = nxt;
       }
     };
-    auto flush_k = [&](int tile) {
+    auto flush_k = [&](int tile) __attribute__((always_inline)) {
       if constexpr (KG)
         if (wave == TA_WAVES - 1) {
           sIdxK[tile & 1][lane] = (uint32_t)kpend * krow_bytes;
@@ -527,7 +539,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     };
     // K and V tiles via LDS DMA (each wave instruction fills 4 whole rows, the
     // lane fetching the 16-byte chunk that belongs at its swizzled position)
-    auto issue = [&](int tile, auto BUF) {
+    auto issue = [&](int tile, auto BUF) __attribute__((always_inline)) {
       constexpr int buf = decltype(BUF)::value;
       uint16_t* sKb = buf ? sK1 : sK0;
       uint16_t* sVb = buf ? sV1 : sV0;
@@ -547,7 +559,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
       }
     };
     // one 64-key tile of the online softmax; MASK: the last, partial tile
-    auto tile_step = [&](auto BUF, int valid, auto MASK) {
+    auto tile_step = [&](auto BUF, int valid, auto MASK) __attribute__((always_inline)) {
       constexpr int buf = decltype(BUF)::value;
       const uint16_t* sKb = buf ? sK1 : sK0;
       // scores of the two 32-key halves as two interleaved MFMA chains, each
@@ -556,7 +568,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
       // spare registers and fed the other through a single buffer, each MFMA
       // of it waiting on its own LDS read.
       f32x16 S[2] = {zero16(), zero16()};
-      auto rdk = [&](int kb, int s) {
+      auto rdk = [&](int kb, int s) __attribute__((always_inline)) {
         return *(const u32x4*)(sKb + sk_off(32 * kb + jl, 2 * s + hh));
       };
       constexpr int KD = 4;  // read-ahead depth in k-steps
@@ -590,7 +602,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
       // every earlier tile) is redone with m moved past its max, the sums so
       // far rescaled (the reference's lazy max, taken only when needed)
       u32x4 pb[4];
-      auto expo = [&](float nm) {
+      auto expo = [&](float nm) __attribute__((always_inline)) {
         float acc = 0.f;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -626,7 +638,105 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     };
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
+    if (tid < 2) {
+      sReady[tid] = 0;
+      sDone[tid] = 0;
+    }
+    if (tid == 0) sAbort = 0;
     __syncthreads();  // runs visible
+    if (qrows <= 32 * (TA_WAVES - 1)) {
+      // the last wave stages every tile (all 16 row groups of K and V) and
+      // publishes it; the consumer waves wait only for the tile they read and
+      // report when they are done with a buffer
+      const int nact = (qrows + 31) >> 5;
+      auto issue_all = [&](int tile, auto BUF) __attribute__((always_inline)) {
+        constexpr int buf = decltype(BUF)::value;
+        uint16_t* sKb = buf ? sK1 : sK0;
+        uint16_t* sVb = buf ? sV1 : sV0;
+#pragma unroll
+        for (int blk = 0; blk < 16; ++blk) {
+          const int row = 4 * blk + (lane >> 4);
+          const uint32_t base = sIdx[buf][row];
+          const uint32_t kbase = KG ? sIdxK[buf][row] : base;
+          const uint32_t offk = kbase + 16u * ((lane & 15) ^ (row & 15));
+          const uint32_t vbase = VG ? sIdxV[buf][row] : base;
+          const uint32_t offv = vbase + 16u * ((lane & 15) ^ sv_swz(row));
+          __builtin_amdgcn_global_load_lds((const glb_void_t*)(kh + offk),
+                                           (lds_void_t*)(sKb + blk * 4 * 128), 16, 0, 0);
+          __builtin_amdgcn_global_load_lds((const glb_void_t*)(vh + offv),
+                                           (lds_void_t*)(sVb + blk * 4 * 128), 16, 0, 0);
+        }
+      };
+      // poll an LDS word until ok(value); bounded (see sAbort)
+      auto spin = [&](int* w, auto ok) __attribute__((always_inline)) {
+        for (int n = 0;; ++n) {
+          if (ok(__hip_atomic_load(w, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP))) return;
+          if (n > T2T_SPIN_CAP ||
+              __hip_atomic_load(&sAbort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) {
+            if (lane == 0)
+              __hip_atomic_store(&sAbort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            return;
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+      };
+      auto publish = [&](int tile) __attribute__((always_inline)) {
+        if (lane == 0)
+          __hip_atomic_store(&sReady[tile & 1], tile + 1, __ATOMIC_RELEASE,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
+      };
+      if (wave == TA_WAVES - 1) {
+        build_idx(0);
+        flush_k(0);
+        issue_all(0, B0{});
+        if (ntile > 1) {
+          build_idx(1);
+          flush_k(1);
+          issue_all(1, B1{});
+        }
+        if (ntile > 2) build_idx(2);
+        __builtin_amdgcn_s_waitcnt(0);
+        publish(0);
+        for (int t = 0; t + 1 < ntile; ++t) {
+          __builtin_amdgcn_s_waitcnt(0);  // tile t + 1 (and the kperm rows of t + 2) landed
+          publish(t + 1);
+          if (t + 2 < ntile) {
+            flush_k(t + 2);
+            const int want = nact * ((t >> 1) + 1);
+            spin(&sDone[t & 1], [&](int v) { return v >= want; });
+            if (t & 1)
+              issue_all(t + 2, B1{});
+            else
+              issue_all(t + 2, B0{});
+            if (t + 3 < ntile) build_idx(t + 3);
+          }
+        }
+      } else if (wave < nact) {
+        auto consume = [&](int tile, auto BUF, int valid, auto MASK) __attribute__((always_inline)) {
+          constexpr int buf = decltype(BUF)::value;
+          spin(&sReady[buf], [&](int v) { return v == tile + 1; });
+          tile_step(BUF, valid, MASK);
+          if (lane == 0)
+            __hip_atomic_fetch_add(&sDone[buf], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        };
+        const int nfull = (kvlen % TA_KT) ? ntile - 1 : ntile;
+        int tile = 0;
+        for (; tile + 2 <= nfull; tile += 2) {
+          consume(tile, B0{}, TA_KT, std::false_type{});
+          consume(tile + 1, B1{}, TA_KT, std::false_type{});
+        }
+        if (tile < nfull) consume(tile++, B0{}, TA_KT, std::false_type{});
+        if (tile < ntile) {
+          const int valid = kvlen - tile * TA_KT;
+          if (tile & 1)
+            consume(tile, B1{}, valid, std::true_type{});
+          else
+            consume(tile, B0{}, valid, std::true_type{});
+        }
+      }
+    } else {
+    // tasks of four waves: every wave stages a quarter of each tile, one
+    // barrier per tile
     build_idx(0);
     flush_k(0);
     if (ntile > 1) {
@@ -641,7 +751,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
     if (ntile > 2) build_idx(2);
     // one full tile held in buffer BUF: consume it, stage the V of the next
     // tile, wait for the next tile's K, then start the tile after it
-    auto body = [&](int tile, auto BUF) {
+    auto body = [&](int tile, auto BUF) __attribute__((always_inline)) {
       constexpr int buf = decltype(BUF)::value;
       if (wave_active) tile_step(BUF, TA_KT, std::false_type{});
       __builtin_amdgcn_s_waitcnt(0);  // K and V DMA of tile + 1 landed (and kperm of tile + 2)
@@ -666,6 +776,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
         tile_step(B1{}, valid, std::true_type{});
       else
         tile_step(B0{}, valid, std::true_type{});
+    }
     }
   }
   const float lt = half_sum(lsum);
