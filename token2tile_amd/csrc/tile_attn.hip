@@ -329,7 +329,7 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
   // done with each buffer, both monotonic
   // sAbort: set when a wait passes T2T_SPIN_CAP polls; every later wait of the
   // work-group then returns at once, so a broken handshake ends the kernel
-  // (with a wrong result) instead of hanging it
+  // (with NaN in the task's output) instead of hanging it
   __shared__ int sReady[2], sDone[2], sAbort;
   __shared__ int wsc[TA_WAVES], wsr[TA_WAVES];
   const int total = H * maxT;
@@ -733,6 +733,9 @@ __global__ __launch_bounds__(TA_WAVES * 64, 2) void attn_kernel(
           else
             consume(tile, B0{}, valid, std::true_type{});
         }
+        // a wait that gave up leaves the output NaN, not silently wrong
+        if (__hip_atomic_load(&sAbort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))
+          lsum = __builtin_nanf("");
       }
     } else {
     // tasks of four waves: every wave stages a quarter of each tile, one
