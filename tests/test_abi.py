@@ -75,3 +75,28 @@ def test_noalloc_select_rejects_oversized_scratch():
     assert L.t2t_score_select_packed_noalloc(p, p, p, p, p, p, p, p, 65, 8192, 4096, None) == 4
     assert b"static scratch" in L.t2t_last_error()
     assert L.t2t_score_select_packed_noalloc(None, p, p, p, p, p, p, p, 1, 8192, 16, None) == 1
+
+
+def test_attention_entry_points_reject_bad_arguments():
+    """The exact-attention and residual entries reject a bad dtype, sizes
+    outside their limits, strides the kernels cannot address and a short
+    workspace, each with its error code, before any launch."""
+    from token2tile_amd import _lib
+    L = _lib.lib()
+    p = ctypes.c_void_p(16)
+    exact = lambda dtype, H, N, CQ: L.t2t_tile_attn_exact(p, p, p, dtype, p, p, p, p, p, p, H, N,
+                                                          CQ, None)
+    assert exact(7, 1, 64, 4) == 1 and b"dtype" in L.t2t_last_error()
+    assert exact(1, 0, 64, 4) == 1
+    assert exact(1, 1, 1 << 24, 4) == 1                   # row indices are 24-bit in LDS
+    assert L.t2t_tail_merge(p, p, p, p, p, p, p, p, p, p, p, p, 1, 2, 64, 4, p, 16, None) == 2
+    assert b"workspace" in L.t2t_last_error()
+
+    def strided(q_rs=128, k_rs=128, N=64, o_rs=128):
+        return L.t2t_tile_attn_exact_orig_gather_kv_strided(
+            p, 0, q_rs, p, 0, k_rs, p, 0, 128, p, 1, p, p, p, p, p, 0, o_rs, p, 1, N, 4, None)
+    assert strided(q_rs=64) == 1 and b"row strides >= 128" in L.t2t_last_error()
+    assert strided(o_rs=132) == 1                         # not a multiple of 8 elements
+    assert strided(k_rs=1 << 20, N=4096) == 1 and b"4 GiB" in L.t2t_last_error()
+    assert L.t2t_resid_merge_inplace_strided(p, 0, 100, p, p, p, p, p, p, p, p, p, 1, 1, 64, 4,
+                                            None) == 1
