@@ -83,7 +83,8 @@ def test_sparse_block_stack(dev):
 
 
 @pytest.mark.gpu
-def test_wan14b_720p_stack_dense_vs_t2t(dev, metrics):
+@pytest.mark.parametrize("structured", [False, True], ids=["random", "structured"])
+def test_wan14b_720p_stack_dense_vs_t2t(dev, metrics, structured):
     """BASELINE config 5 at full size: the Wan2.1-14B block stack (40 blocks,
     hidden 5120, 40 heads, FFN 13824, 75,600 video + 512 text tokens, random
     bf16 weights), one dense step and two T2T steps through the backend with
@@ -91,15 +92,20 @@ def test_wan14b_720p_stack_dense_vs_t2t(dev, metrics):
     rebuild) and step 13 (a mask_refresh=4 reuse step).  Checks a finite
     output, the T2T output against the dense one (cosine), that the fitted
     state persists from step 12 to step 13 without a refit, and records both
-    step times."""
+    step times.  ``structured``: key weights tied to the query weights and a
+    spatially smooth latent, so that attention is local (smaller unions)."""
     import time
     cfg = dit.DiTConfig()
     assert (cfg.blocks, cfg.hidden, cfg.heads, cfg.ffn, cfg.tokens) == (40, 5120, 40, 13824, 75600)
     torch.manual_seed(0)
-    model = dit.WanDiT(cfg, sparse=True, device=dev)
+    model = dit.WanDiT(cfg, sparse=True, device=dev, tie=0.9 if structured else 0.0)
     impls = [blk.attn_impl for blk in model.blocks]
     g = torch.Generator(device=dev).manual_seed(1)
-    x = torch.randn(1, cfg.tokens, cfg.hidden, generator=g, device=dev, dtype=torch.bfloat16)
+    if structured:
+        x = dit.smooth_latent(cfg, g, dev)
+    else:
+        x = torch.randn(1, cfg.tokens, cfg.hidden, generator=g, device=dev, dtype=torch.bfloat16)
+    tag = "dit720p_structured" if structured else "dit720p"
     ctx = torch.randn(1, cfg.context_tokens, cfg.hidden, generator=g, device=dev,
                       dtype=torch.bfloat16)
     t = 0.1 * torch.randn(1, cfg.hidden, generator=g, device=dev, dtype=torch.bfloat16)
@@ -115,7 +121,7 @@ def test_wan14b_720p_stack_dense_vs_t2t(dev, metrics):
         blk.attn_impl = None
     timed(lambda: model(x, t, ctx))                     # warm-up (library set-up)
     yd, dense_ms = timed(lambda: model(x, t, ctx))
-    print(f"[dit720p] dense step {dense_ms:.0f} ms", flush=True)
+    print(f"[{tag}] dense step {dense_ms:.0f} ms", flush=True)
     for blk, impl in zip(model.blocks, impls):
         blk.attn_impl = impl
     from token2tile_amd.backend.t2t_attn import T2TAttentionMetadataBuilder, T2TRequestCache
@@ -124,7 +130,7 @@ def test_wan14b_720p_stack_dense_vs_t2t(dev, metrics):
     for step in (12, 13):
         md = builder.build(step_index=step, total_steps=50, cache=cache, profile_name="auto")
         outs[step], ms[step] = timed(lambda m=md: model(x, t, ctx, lambda i: m))
-        print(f"[dit720p] t2t step {step} {ms[step]:.0f} ms", flush=True)
+        print(f"[{tag}] t2t step {step} {ms[step]:.0f} ms", flush=True)
         if step == 12:
             assert len(cache.states) == cfg.blocks          # one fitted state per layer
             fitted = {k_: st["Uq"] for k_, st in cache.states.items()}
@@ -132,9 +138,9 @@ def test_wan14b_720p_stack_dense_vs_t2t(dev, metrics):
     for step, y in outs.items():
         assert bool(torch.isfinite(y).all())
         cs = torch.nn.functional.cosine_similarity(y.float().flatten(), yd.float().flatten(), dim=0)
-        metrics[f"dit720p_cos_t2t_step{step}_vs_dense"] = round(float(cs), 5)
+        metrics[f"{tag}_cos_t2t_step{step}_vs_dense"] = round(float(cs), 5)
         assert cs > 0.999, (step, float(cs))
-    metrics["dit720p_dense_step_ms"] = round(dense_ms, 1)
-    metrics["dit720p_t2t_step12_fit_rebuild_ms"] = round(ms[12], 1)
-    metrics["dit720p_t2t_step13_reuse_ms"] = round(ms[13], 1)
-    metrics["dit720p_step13_speedup_vs_dense"] = round(dense_ms / ms[13], 3)
+    metrics[f"{tag}_dense_step_ms"] = round(dense_ms, 1)
+    metrics[f"{tag}_t2t_step12_fit_rebuild_ms"] = round(ms[12], 1)
+    metrics[f"{tag}_t2t_step13_reuse_ms"] = round(ms[13], 1)
+    metrics[f"{tag}_step13_speedup_vs_dense"] = round(dense_ms / ms[13], 3)

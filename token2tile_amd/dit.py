@@ -141,7 +141,7 @@ class WanDiT(torch.nn.Module):
     head are outside the attention path and omitted; the latent enters as
     [1, N, hidden] tokens)."""
 
-    def __init__(self, cfg: DiTConfig, sparse: bool, device, dtype=torch.bfloat16):
+    def __init__(self, cfg: DiTConfig, sparse: bool, device, dtype=torch.bfloat16, tie=0.0):
         super().__init__()
         self.cfg = cfg
         impls = [None] * cfg.blocks
@@ -155,6 +155,13 @@ class WanDiT(torch.nn.Module):
             if isinstance(m, torch.nn.Linear):
                 torch.nn.init.normal_(m.weight, std=m.in_features ** -0.5)
                 torch.nn.init.zeros_(m.bias)
+        if tie > 0:
+            # self-attention key weights tied to the query weights (same scale):
+            # W_k = tie W_q + sqrt(1 - tie^2) W_k, so q_i . k_j is large for
+            # similar tokens and attention follows the latent's structure
+            with torch.no_grad():
+                for blk in self.blocks:
+                    blk.k.weight.mul_(math.sqrt(1.0 - tie * tie)).add_(tie * blk.q.weight)
         self.to(dtype)
         self.rope = rope_tables(cfg, device)
 
@@ -166,15 +173,39 @@ class WanDiT(torch.nn.Module):
         return x
 
 
-def run(cfg: DiTConfig, steps, device, *, sparse: bool, profile="auto", budget_kw=None, seed=0):
+def smooth_latent(cfg: DiTConfig, g, device, components=32, noise=0.3):
+    """[1, N, hidden] tokens that vary smoothly over the (frame, height,
+    width) grid: a sum of low-frequency plane waves, each along its own
+    random direction of the hidden space, plus white noise."""
+    f, h, w = cfg.grid
+    pos = torch.stack(torch.meshgrid(torch.arange(f), torch.arange(h), torch.arange(w),
+                                     indexing="ij"), dim=-1).reshape(-1, 3).to(device).float()
+    pos = pos / torch.tensor([f, h, w], device=device, dtype=torch.float32)
+    freq = 3.0 * torch.randn(3, components, generator=g, device=device)
+    phase = 2 * math.pi * torch.rand(components, generator=g, device=device)
+    dirs = torch.randn(components, cfg.hidden, generator=g, device=device)
+    waves = torch.sin(2 * math.pi * pos @ freq + phase)                 # [N, components]
+    x = waves @ dirs / math.sqrt(components)
+    x += noise * torch.randn(x.shape, generator=g, device=device)
+    return x[None].to(torch.bfloat16)
+
+
+def run(cfg: DiTConfig, steps, device, *, sparse: bool, profile="auto", budget_kw=None, seed=0,
+        structured=False):
     """Time one forward (one CFG branch) of the block stack per denoising step
     index in ``steps``; returns {step: ms}.  With ``sparse`` the self-attention
     goes through the T2T backend, whose dense prefix, budget windows and
-    mask-refresh schedule follow the step index."""
+    mask-refresh schedule follow the step index.  ``structured``: key weights
+    tied to the query weights (0.9) and a spatially smooth latent, so that
+    attention is local, as in trained video models (random weights and white
+    noise give near-uniform attention, whose unions hold most keys)."""
     torch.manual_seed(seed)
-    model = WanDiT(cfg, sparse, device)
+    model = WanDiT(cfg, sparse, device, tie=0.9 if structured else 0.0)
     g = torch.Generator(device=device).manual_seed(seed + 1)
-    x = torch.randn(1, cfg.tokens, cfg.hidden, generator=g, device=device, dtype=torch.bfloat16)
+    if structured:
+        x = smooth_latent(cfg, g, device)
+    else:
+        x = torch.randn(1, cfg.tokens, cfg.hidden, generator=g, device=device, dtype=torch.bfloat16)
     ctx = torch.randn(1, cfg.context_tokens, cfg.hidden, generator=g, device=device,
                       dtype=torch.bfloat16)
     t_emb = 0.1 * torch.randn(1, cfg.hidden, generator=g, device=device, dtype=torch.bfloat16)
@@ -207,12 +238,14 @@ def main(argv=None):
     p.add_argument("--blocks", type=int, default=40)
     p.add_argument("--per-window", type=int, default=4,
                    help="sparse steps timed per budget window (after the initial step 12)")
+    p.add_argument("--structured", action="store_true",
+                   help="tied q/k weights and a smooth latent (local attention); default: random")
     args = p.parse_args(argv)
     if not torch.cuda.is_available():
         sys.exit("the DiT harness needs a ROCm GPU")
     dev = torch.device("cuda", 0)
     cfg = DiTConfig(blocks=args.blocks)
-    dense = run(cfg, [0, 1, 2], dev, sparse=False)
+    dense = run(cfg, [0, 1, 2], dev, sparse=False, structured=args.structured)
     d_ms = (dense[1] + dense[2]) / 2
     torch.cuda.empty_cache()
     # step 12 fits the projections and centroids (init_state) and rebuilds;
@@ -222,7 +255,7 @@ def main(argv=None):
     for lo, hi in WINDOWS:
         first = lo + 1 if lo == 12 else lo
         steps += list(range(first, min(hi, first + args.per_window)))
-    sparse = run(cfg, steps, dev, sparse=True)
+    sparse = run(cfg, steps, dev, sparse=True, structured=args.structured)
     win_ms = []
     for lo, hi in WINDOWS:
         ts = [sparse[s] for s in steps if lo <= s < hi and s != 12]
@@ -235,7 +268,9 @@ def main(argv=None):
     out = {"metric": "Wan2.1-14B DiT denoising step (one CFG branch), ms",
            "config": {"blocks": cfg.blocks, "hidden": cfg.hidden, "heads": cfg.heads,
                       "ffn": cfg.ffn, "tokens": cfg.tokens, "context_tokens": cfg.context_tokens,
-                      "dtype": "bf16", "weights": "random", "attention_profile": "auto"},
+                      "dtype": "bf16",
+                      "weights": "random, k tied to q (0.9), smooth latent" if args.structured
+                      else "random", "attention_profile": "auto"},
            "dense_ms_per_step": round(d_ms, 1),
            "t2t_step_ms": {str(k): round(v, 1) for k, v in sparse.items()},
            "t2t_ms_per_step_by_window": [round(w, 1) for w in win_ms],
