@@ -501,9 +501,10 @@ __global__ __launch_bounds__(SEL_WAVES * 64) void select_main_kernel(
 // over them, and the next batch's query rows load while the current batch is
 // being selected.  LDS: the batch's keys (128 KB; 16-byte chunks XOR
 // swizzled by row instead of padded), twelve 1.75 KB window histograms and the
-// cluster sizes.  The centroid fragments are reloaded from L2 per batch: held
+// cluster sizes.  The centroid fragments are reloaded from L2 per batch (held
 // across batches they would push the kernel past the 168 registers of three
-// waves per SIMD.
+// waves per SIMD), each wave issuing the next batch's loads just before the
+// batch's closing barrier, so that their latency hides behind it.
 // ---------------------------------------------------------------------------
 #define SF_WAVES 12
 #define SF_ROWS 32
@@ -583,6 +584,11 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
     }
   };
 
+  // the wave's centroid fragments of the next batch, loaded while the wave
+  // waits at the end of the previous batch (its selection registers are dead
+  // there), so their L2 latency hides behind that barrier
+  u32x4 ca0[SF_TILES], ca1[SF_TILES];
+  load_ca(ca0, ca1);
   if (threadIdx.x < 2) sNext[threadIdx.x] = 0;
   for (int c = threadIdx.x; c < SEL_NC; c += SF_WAVES * 64) sSz[c] = kcounts[(size_t)h * SEL_NC + c];
   for (int b = 0; b < SF_BATCHES; ++b) {
@@ -590,8 +596,6 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
     if (j0 >= lim) break;
     {  // scores of rows j0 .. j0 + 31 against the wave's centroids -> keys in LDS
       uint16_t* krow = sKey + jl * SF_PITCH + 4 * hh;
-      u32x4 ca0[SF_TILES], ca1[SF_TILES];  // reloaded (from L2) for each batch
-      load_ca(ca0, ca1);
 #pragma unroll
       for (int cb = 0; cb < SF_TILES; ++cb) {
         if (cb >= ntl) break;  // wave-uniform
@@ -682,6 +686,7 @@ __global__ __launch_bounds__(SF_WAVES * 64, 1) void score_select_kernel(
       klo = vstar - SEL_BOUND_MARGIN;
       if (l == 0) rowcnt[(size_t)h * N + qp[j]] = rc;
     }
+    load_ca(ca0, ca1);  // the next batch's fragments (see above)
     __syncthreads();  // the next batch overwrites the keys
   }
   if (t >= 0) flush_union(acc, uh + (size_t)t * (SEL_NC / 32));
